@@ -1,0 +1,30 @@
+"""MI355X (gfx950) attention path of anima-flat's DiT, as hand-written HIP kernels.
+
+Drop-in modules, same public signatures as the reference:
+  attention      <- src/attention.py      (use_fa4, attention, cross_attention_trimmed,
+                                            ops anima_flat::fa_fwd / fa_fwd_nolse / fa_fwd_k / fa_bwd)
+  kernels.rope   <- src/kernels/rope.py   (qkv_norm_rope, head_norm and their ops)
+  kernels.ctx_scale <- src/kernels/ctx_scale.py (ctx_scale and its ops)
+  context        <- src/model.py:51-119, 247-254 (rope_tables, Context, context trimming)
+
+All compute runs in libanima_attn.so (csrc/, C ABI in include/anima_attn.h),
+loaded through ctypes by _lib.py. There is no CPU or SDPA fallback.
+"""
+
+from . import _lib  # noqa: F401
+from .attention import attention, cross_attention_trimmed, use_fa4  # noqa: F401
+from .context import Context, rope_tables, trim_context  # noqa: F401
+from .kernels.ctx_scale import ctx_scale  # noqa: F401
+from .kernels.rope import head_norm, qkv_norm_rope  # noqa: F401
+
+__all__ = [
+    "Context",
+    "attention",
+    "cross_attention_trimmed",
+    "ctx_scale",
+    "head_norm",
+    "qkv_norm_rope",
+    "rope_tables",
+    "trim_context",
+    "use_fa4",
+]

@@ -1,0 +1,90 @@
+"""Builds libanima_attn.so from csrc/*.hip with hipcc for gfx950.
+
+Objects go to `_build/` next to this file and the library to
+`libanima_attn.so` in this directory, where `_lib.py` loads it from. Every
+source compiles in parallel; nothing is cached between calls (the caller asks
+for a build, so it gets one).
+
+Run as a script to build: ``python anima-flat_amd/build.py``.
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+CSRC = HERE / "csrc"
+BUILD = HERE / "_build"
+LIB_NAME = "libanima_attn.so"
+LIB_PATH = HERE / LIB_NAME
+SOURCES = ("abi.hip", "prologue.hip", "ctx_scale.hip", "attn_fwd.hip", "attn_bwd.hip")
+ARCH = "gfx950"
+
+# Packed fp32 VALU forms are disabled for all device code: the compiler then
+# emits only scalar v_fma_f32/v_mul_f32 for float arithmetic.
+DEVICE_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-Xclang",
+    "-target-feature",
+    "-Xclang",
+    "-packed-fp32-ops",
+]
+
+
+def hipcc() -> str:
+    """Path of hipcc (ROCM_PATH/bin, then PATH)."""
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    cand = Path(rocm) / "bin" / "hipcc"
+    if cand.exists():
+        return str(cand)
+    found = shutil.which("hipcc")
+    if not found:
+        raise RuntimeError("hipcc not found: set ROCM_PATH or put hipcc on PATH")
+    return found
+
+
+def _run(cmd: list[str]) -> None:
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        # hipcc's host pass warns about the packed-fp32 feature; keep real errors.
+        err = "\n".join(
+            line for line in proc.stderr.splitlines() if "packed-fp32-ops" not in line
+        )
+        raise RuntimeError(f"command failed ({proc.returncode}): {' '.join(cmd)}\n{err}")
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile every source and link libanima_attn.so; returns the library path."""
+    cc = hipcc()
+    BUILD.mkdir(exist_ok=True)
+    objs = []
+    cmds = []
+    for src in SOURCES:
+        obj = BUILD / (Path(src).stem + ".o")
+        objs.append(str(obj))
+        cmds.append([cc, *DEVICE_FLAGS, "-c", str(CSRC / src), "-o", str(obj)])
+    workers = max(1, min(len(cmds), os.cpu_count() or 1, 8))
+    with ThreadPoolExecutor(workers) as pool:
+        for cmd, _ in zip(cmds, pool.map(_run, cmds)):
+            if verbose:
+                print(" ".join(cmd), flush=True)
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    link = [cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *objs]
+    if verbose:
+        print(" ".join(link), flush=True)
+    _run(link)
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    path = build(verbose="-v" in sys.argv)
+    print(path)

@@ -1,0 +1,410 @@
+// QK-RMSNorm + rotate-half RoPE prologue and per-head RMSNorm, forward and
+// backward, for head_dim 128 (two halves of 64).
+//
+// Work unit: one "section" = one (token, head) slice of 128 bf16 = 256 bytes,
+// handled by a group of 8 lanes. Lane j of the group holds elements
+// [8j, 8j+8) of the first half and [64+8j, 64+8j+8) of the second half, so
+// every rotate-half pair (x[i], x[i+64]) sits in one lane and each lane moves
+// two 16-byte chunks. The RMS sum is reduced over the 8 lanes of the group.
+//
+// These kernels are HBM-bound: per section they read 256 B and write 256 B;
+// cos/sin rows (2 x 256 B per token) and the weights stay in L2/L1.
+#include "aa_common.h"
+
+namespace aa {
+
+constexpr int kHd = 128;
+constexpr int kHalf = 64;
+
+struct Section {
+  float a[8];
+  float b[8];
+};
+
+__device__ __forceinline__ void load_section(const bf16* src, int j, Section& s) {
+  unpack8(ld16(src + 8 * j), s.a);
+  unpack8(ld16(src + kHalf + 8 * j), s.b);
+}
+
+__device__ __forceinline__ void load_w(const float* w, int j, float* wa, float* wb) {
+  f32x4 w0 = ldf4(w + 8 * j), w1 = ldf4(w + 8 * j + 4);
+  f32x4 w2 = ldf4(w + kHalf + 8 * j), w3 = ldf4(w + kHalf + 8 * j + 4);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    wa[i] = w0[i];
+    wa[i + 4] = w1[i];
+    wb[i] = w2[i];
+    wb[i + 4] = w3[i];
+  }
+}
+
+__device__ __forceinline__ void load_rot(const float* cos, const float* sin, int64_t pos, int j,
+                                         float* c, float* s) {
+  const float* cp = cos + pos * kHalf + 8 * j;
+  const float* sp = sin + pos * kHalf + 8 * j;
+  f32x4 c0 = ldf4(cp), c1 = ldf4(cp + 4), s0 = ldf4(sp), s1 = ldf4(sp + 4);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    c[i] = c0[i];
+    c[i + 4] = c1[i];
+    s[i] = s0[i];
+    s[i + 4] = s1[i];
+  }
+}
+
+// Forward of one section: rstd over 128 values, y = bf16(x * rstd * w), then
+// optional rotation out_a = y_a cos - y_b sin, out_b = y_b cos + y_a sin
+// (the order of src/kernels/rope.py:39-58).
+template <bool ROTATE>
+__device__ __forceinline__ void norm_section(const bf16* src, bf16* dst, const float* w,
+                                             const float* cos, const float* sin, int64_t pos,
+                                             int j, float eps) {
+  Section x;
+  load_section(src, j, x);
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ss += x.a[i] * x.a[i] + x.b[i] * x.b[i];
+  ss = group_sum<8>(ss);
+  const float rstd = rsqrtf(ss / (float)kHd + eps);
+  float wa[8], wb[8];
+  load_w(w, j, wa, wb);
+  float oa[8], ob[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    oa[i] = round_bf16(x.a[i] * rstd * wa[i]);
+    ob[i] = round_bf16(x.b[i] * rstd * wb[i]);
+  }
+  if constexpr (ROTATE) {
+    float c[8], s[8];
+    load_rot(cos, sin, pos, j, c, s);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float ya = oa[i], yb = ob[i];
+      oa[i] = ya * c[i] - yb * s[i];
+      ob[i] = yb * c[i] + ya * s[i];
+    }
+  }
+  st16(dst + 8 * j, pack8(oa));
+  st16(dst + kHalf + 8 * j, pack8(ob));
+}
+
+// qkv [ntok, 3*H*128] -> q, k [ntok, H, 128] (+ v copy). Sections of a token:
+// [0,H) q heads, [H,2H) k heads, [2H,3H) v heads (only when v != nullptr).
+template <bool WITH_V>
+__global__ __launch_bounds__(256) void qkv_norm_rope_fwd_kernel(
+    const bf16* __restrict__ qkv, bf16* __restrict__ q, bf16* __restrict__ k,
+    bf16* __restrict__ v, const float* __restrict__ qw, const float* __restrict__ kw,
+    const float* __restrict__ cos, const float* __restrict__ sin, int64_t ntok, int64_t S,
+    int H, float eps) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int j = (int)(gid & 7);
+  const int64_t group = gid >> 3;
+  const int nsec = WITH_V ? 3 * H : 2 * H;
+  const int64_t token = group / nsec;
+  if (token >= ntok) return;
+  const int sec = (int)(group - token * nsec);
+  const int which = sec / H;
+  const int head = sec - which * H;
+  const int64_t width = (int64_t)H * kHd;
+  const bf16* src = qkv + token * 3 * width + which * width + head * kHd;
+  const int64_t dst_off = token * width + head * kHd;
+  if (WITH_V && which == 2) {
+    st16(v + dst_off + 8 * j, ld16(src + 8 * j));
+    st16(v + dst_off + kHalf + 8 * j, ld16(src + kHalf + 8 * j));
+    return;
+  }
+  const int64_t pos = token % S;
+  norm_section<true>(src, (which == 0 ? q : k) + dst_off, which == 0 ? qw : kw, cos, sin, pos, j,
+                     eps);
+}
+
+// x [ntok, H*128] -> y [ntok, H, 128].
+__global__ __launch_bounds__(256) void head_norm_fwd_kernel(const bf16* __restrict__ x,
+                                                            bf16* __restrict__ y,
+                                                            const float* __restrict__ w,
+                                                            int64_t nsec, float eps) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t sec = gid >> 3;
+  if (sec >= nsec) return;
+  const int j = (int)(gid & 7);
+  norm_section<false>(x + sec * kHd, y + sec * kHd, w, nullptr, nullptr, 0, j, eps);
+}
+
+// ------------------------------------------------------------- backward --
+
+// Backward of one section (src/kernels/rope.py:244-274): rotate dy back,
+// then dx = rstd * (u - xhat * mean(u * xhat)) with u = dy' * w; returns the
+// per-dimension weight-gradient terms dy' * xhat through ga/gb.
+template <bool ROTATE>
+__device__ __forceinline__ void norm_section_bwd(const bf16* src, const bf16* dy, bf16* dx,
+                                                 const float* w, const float* cos,
+                                                 const float* sin, int64_t pos, int j, float eps,
+                                                 float* ga, float* gb) {
+  Section x, d;
+  load_section(src, j, x);
+  load_section(dy, j, d);
+  if constexpr (ROTATE) {
+    float c[8], s[8];
+    load_rot(cos, sin, pos, j, c, s);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float da = d.a[i], db = d.b[i];
+      d.a[i] = da * c[i] + db * s[i];
+      d.b[i] = db * c[i] - da * s[i];
+    }
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ss += x.a[i] * x.a[i] + x.b[i] * x.b[i];
+  ss = group_sum<8>(ss);
+  const float rstd = rsqrtf(ss / (float)kHd + eps);
+  float wa[8], wb[8];
+  load_w(w, j, wa, wb);
+  float xa[8], xb[8], ua[8], ub[8];
+  float dot = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    xa[i] = x.a[i] * rstd;
+    xb[i] = x.b[i] * rstd;
+    ua[i] = d.a[i] * wa[i];
+    ub[i] = d.b[i] * wb[i];
+    dot += ua[i] * xa[i] + ub[i] * xb[i];
+  }
+  const float c = group_sum<8>(dot) / (float)kHd;
+  float oa[8], ob[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    oa[i] = rstd * (ua[i] - xa[i] * c);
+    ob[i] = rstd * (ub[i] - xb[i] * c);
+    ga[i] += d.a[i] * xa[i];
+    gb[i] += d.b[i] * xb[i];
+  }
+  st16(dx + 8 * j, pack8(oa));
+  st16(dx + kHalf + 8 * j, pack8(ob));
+}
+
+constexpr int kBwdThreads = 256;
+constexpr int kBwdGroups = kBwdThreads / 8;  // 32 sections in flight per block
+
+// One block per chunk of `rows` consecutive tokens. Normalised sections per
+// token: NWHICH*H (q then k for the QKV prologue, one set for head_norm).
+// Group g handles sections g, g+32, ... of every token in the chunk and keeps
+// per-lane weight-gradient sums for each of the NWHICH weights; the block
+// then reduces them over groups in a fixed order into
+// partial[chunk][which][128].
+template <bool ROTATE, int NWHICH>
+__global__ __launch_bounds__(kBwdThreads) void norm_bwd_kernel(
+    const bf16* __restrict__ x, const bf16* __restrict__ dy0, const bf16* __restrict__ dy1,
+    const bf16* __restrict__ dv, bf16* __restrict__ dx, const float* __restrict__ w0,
+    const float* __restrict__ w1, const float* __restrict__ cos, const float* __restrict__ sin,
+    float* __restrict__ partial, int64_t ntok, int64_t S, int H, int rows, float eps) {
+  __shared__ float red[kBwdGroups][NWHICH][kHd];
+  const int tid = threadIdx.x;
+  const int j = tid & 7;
+  const int g = tid >> 3;
+  const int64_t width = (int64_t)H * kHd;
+  // x and dx rows hold NWHICH (+1 with dv) sections of width H*128 each.
+  const int64_t xrow = dv ? 3 * width : NWHICH * width;
+  float acc[NWHICH][16];
+#pragma unroll
+  for (int wi = 0; wi < NWHICH; ++wi)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[wi][i] = 0.f;
+
+  const int64_t first = (int64_t)blockIdx.x * rows;
+  for (int r = 0; r < rows; ++r) {
+    const int64_t token = first + r;
+    if (token >= ntok) break;
+    const int64_t pos = token % S;
+    for (int sec = g; sec < NWHICH * H; sec += kBwdGroups) {
+      const int which = sec / H;
+      const int head = sec - which * H;
+      const bf16* src = x + token * xrow + which * width + head * kHd;
+      const bf16* dy = (which == 0 ? dy0 : dy1) + token * width + head * kHd;
+      bf16* out = dx + token * xrow + which * width + head * kHd;
+      const float* w = which == 0 ? w0 : w1;
+      if (NWHICH == 1 || which == 0) {
+        norm_section_bwd<ROTATE>(src, dy, out, w, cos, sin, pos, j, eps, acc[0], acc[0] + 8);
+      } else {
+        norm_section_bwd<ROTATE>(src, dy, out, w, cos, sin, pos, j, eps, acc[NWHICH - 1],
+                                 acc[NWHICH - 1] + 8);
+      }
+    }
+    if (dv) {  // dV passes through the prologue unchanged: copy it into dqkv.
+      for (int c = tid; c < (int)(width / 8); c += kBwdThreads) {
+        st16(dx + token * xrow + 2 * width + 8 * c, ld16(dv + token * width + 8 * c));
+      }
+    }
+  }
+#pragma unroll
+  for (int wi = 0; wi < NWHICH; ++wi) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      red[g][wi][8 * j + i] = acc[wi][i];
+      red[g][wi][kHalf + 8 * j + i] = acc[wi][8 + i];
+    }
+  }
+  __syncthreads();
+  for (int o = tid; o < NWHICH * kHd; o += kBwdThreads) {
+    const int wi = o / kHd, dim = o % kHd;
+    float s = 0.f;
+    for (int gg = 0; gg < kBwdGroups; ++gg) s += red[gg][wi][dim];
+    partial[((int64_t)blockIdx.x * NWHICH + wi) * kHd + dim] = s;
+  }
+}
+
+// Sums partial[nchunk][n] over chunks in a fixed order: 4 interleaved lanes of
+// chunks per output, combined in order. n <= 256.
+__global__ __launch_bounds__(1024) void reduce_partials_kernel(const float* __restrict__ partial,
+                                                               int64_t nchunk, int n,
+                                                               float* __restrict__ out0,
+                                                               float* __restrict__ out1) {
+  __shared__ float red[4][256];
+  const int o = threadIdx.x & 255;
+  const int p = threadIdx.x >> 8;
+  float s = 0.f;
+  if (o < n) {
+    for (int64_t c = p; c < nchunk; c += 4) s += partial[c * n + o];
+  }
+  red[p][o] = s;
+  __syncthreads();
+  if (p == 0 && o < n) {
+    const float t = ((red[0][o] + red[1][o]) + red[2][o]) + red[3][o];
+    if (o < kHd) out0[o] = t;
+    else out1[o - kHd] = t;
+  }
+}
+
+__global__ void zero_f32_kernel(float* __restrict__ a, float* __restrict__ b, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) {
+    a[i] = 0.f;
+    b[i] = 0.f;
+  }
+}
+
+constexpr int kBwdRows = 16;
+
+static int64_t bwd_chunks(int64_t B, int64_t S) { return (B * S + kBwdRows - 1) / kBwdRows; }
+
+static int check_common(int64_t B, int64_t S, int64_t H, int64_t hd, int dtype) {
+  if (dtype != AA_DTYPE_BF16) return fail(AA_EUNSUPPORTED, "only bf16 activations are implemented");
+  if (hd != kHd) return fail(AA_EUNSUPPORTED, "head_dim must be 128");
+  if (B < 0 || S < 0 || H <= 0 || H > 4096) return fail(AA_EINVAL, "bad B/S/H");
+  return AA_OK;
+}
+
+}  // namespace aa
+
+using namespace aa;
+
+extern "C" int aa_qkv_norm_rope_fwd(const void* qkv, void* q, void* k, void* v,
+                                    const float* q_weight, const float* k_weight,
+                                    const float* cos, const float* sin, int64_t B, int64_t S,
+                                    int64_t H, int64_t hd, float eps, int dtype, void* stream) {
+  clear_error();
+  if (int rc = check_common(B, S, H, hd, dtype)) return rc;
+  if (B * S == 0) return AA_OK;
+  if (!qkv || !q || !k || !q_weight || !k_weight || !cos || !sin)
+    return fail(AA_EINVAL, "qkv_norm_rope_fwd: null pointer");
+  if (!aligned16(qkv) || !aligned16(q) || !aligned16(k) || (v && !aligned16(v)) ||
+      !aligned16(q_weight) || !aligned16(k_weight) || !aligned16(cos) || !aligned16(sin))
+    return fail(AA_EINVAL, "qkv_norm_rope_fwd: pointers must be 16-byte aligned");
+  const int64_t ntok = B * S;
+  const int64_t lanes = ntok * (v ? 3 : 2) * H * 8;
+  const dim3 grid((unsigned)((lanes + 255) / 256));
+  hipStream_t st = (hipStream_t)stream;
+  if (v) {
+    qkv_norm_rope_fwd_kernel<true><<<grid, 256, 0, st>>>(
+        (const bf16*)qkv, (bf16*)q, (bf16*)k, (bf16*)v, q_weight, k_weight, cos, sin, ntok, S,
+        (int)H, eps);
+  } else {
+    qkv_norm_rope_fwd_kernel<false><<<grid, 256, 0, st>>>(
+        (const bf16*)qkv, (bf16*)q, (bf16*)k, nullptr, q_weight, k_weight, cos, sin, ntok, S,
+        (int)H, eps);
+  }
+  return check_launch("qkv_norm_rope_fwd");
+}
+
+extern "C" int aa_head_norm_fwd(const void* x, void* y, const float* weight, int64_t B, int64_t S,
+                                int64_t H, int64_t hd, float eps, int dtype, void* stream) {
+  clear_error();
+  if (int rc = check_common(B, S, H, hd, dtype)) return rc;
+  if (B * S == 0) return AA_OK;
+  if (!x || !y || !weight) return fail(AA_EINVAL, "head_norm_fwd: null pointer");
+  if (!aligned16(x) || !aligned16(y) || !aligned16(weight))
+    return fail(AA_EINVAL, "head_norm_fwd: pointers must be 16-byte aligned");
+  const int64_t nsec = B * S * H;
+  const dim3 grid((unsigned)((nsec * 8 + 255) / 256));
+  head_norm_fwd_kernel<<<grid, 256, 0, (hipStream_t)stream>>>((const bf16*)x, (bf16*)y, weight,
+                                                              nsec, eps);
+  return check_launch("head_norm_fwd");
+}
+
+extern "C" size_t aa_qkv_norm_rope_bwd_workspace(int64_t B, int64_t S, int64_t H, int64_t hd) {
+  (void)H;
+  return (size_t)bwd_chunks(B, S) * 2 * (size_t)hd * sizeof(float);
+}
+
+extern "C" size_t aa_head_norm_bwd_workspace(int64_t B, int64_t S, int64_t H, int64_t hd) {
+  (void)H;
+  return (size_t)bwd_chunks(B, S) * (size_t)hd * sizeof(float);
+}
+
+extern "C" int aa_qkv_norm_rope_bwd(const void* qkv, const void* dq, const void* dk,
+                                    const void* dv, void* dqkv, const float* q_weight,
+                                    const float* k_weight, const float* cos, const float* sin,
+                                    float* dq_weight, float* dk_weight, void* workspace,
+                                    size_t workspace_bytes, int64_t B, int64_t S, int64_t H,
+                                    int64_t hd, float eps, int dtype, void* stream) {
+  clear_error();
+  if (int rc = check_common(B, S, H, hd, dtype)) return rc;
+  if (!qkv || !dq || !dk || !dv || !dqkv || !q_weight || !k_weight || !cos || !sin ||
+      !dq_weight || !dk_weight)
+    return fail(AA_EINVAL, "qkv_norm_rope_bwd: null pointer");
+  if (!aligned16(qkv) || !aligned16(dq) || !aligned16(dk) || !aligned16(dv) ||
+      !aligned16(dqkv) || !aligned16(q_weight) || !aligned16(k_weight) || !aligned16(cos) ||
+      !aligned16(sin))
+    return fail(AA_EINVAL, "qkv_norm_rope_bwd: pointers must be 16-byte aligned");
+  const int64_t nchunk = bwd_chunks(B, S);
+  if (nchunk > 0 && (!workspace || workspace_bytes < aa_qkv_norm_rope_bwd_workspace(B, S, H, hd)))
+    return fail(AA_EINVAL, "qkv_norm_rope_bwd: workspace too small");
+  hipStream_t st = (hipStream_t)stream;
+  if (nchunk == 0) {  // no tokens: weight gradients are zero
+    zero_f32_kernel<<<1, kHd, 0, st>>>(dq_weight, dk_weight, kHd);
+    return check_launch("qkv_norm_rope_bwd zero");
+  }
+  float* partial = (float*)workspace;
+  norm_bwd_kernel<true, 2><<<dim3((unsigned)nchunk), kBwdThreads, 0, st>>>(
+      (const bf16*)qkv, (const bf16*)dq, (const bf16*)dk, (const bf16*)dv, (bf16*)dqkv,
+      q_weight, k_weight, cos, sin, partial, B * S, S, (int)H, kBwdRows, eps);
+  if (int rc = check_launch("qkv_norm_rope_bwd")) return rc;
+  reduce_partials_kernel<<<1, 1024, 0, st>>>(partial, nchunk, 2 * kHd, dq_weight, dk_weight);
+  return check_launch("qkv_norm_rope_bwd reduce");
+}
+
+extern "C" int aa_head_norm_bwd(const void* x, const void* dy, void* dx, const float* weight,
+                                float* dweight, void* workspace, size_t workspace_bytes, int64_t B,
+                                int64_t S, int64_t H, int64_t hd, float eps, int dtype,
+                                void* stream) {
+  clear_error();
+  if (int rc = check_common(B, S, H, hd, dtype)) return rc;
+  if (!x || !dy || !dx || !weight || !dweight) return fail(AA_EINVAL, "head_norm_bwd: null pointer");
+  if (!aligned16(x) || !aligned16(dy) || !aligned16(dx) || !aligned16(weight))
+    return fail(AA_EINVAL, "head_norm_bwd: pointers must be 16-byte aligned");
+  const int64_t nchunk = bwd_chunks(B, S);
+  if (nchunk > 0 && (!workspace || workspace_bytes < aa_head_norm_bwd_workspace(B, S, H, hd)))
+    return fail(AA_EINVAL, "head_norm_bwd: workspace too small");
+  hipStream_t st = (hipStream_t)stream;
+  if (nchunk == 0) {
+    zero_f32_kernel<<<1, kHd, 0, st>>>(dweight, dweight, kHd);
+    return check_launch("head_norm_bwd zero");
+  }
+  float* partial = (float*)workspace;
+  norm_bwd_kernel<false, 1><<<dim3((unsigned)nchunk), kBwdThreads, 0, st>>>(
+      (const bf16*)x, (const bf16*)dy, nullptr, nullptr, (bf16*)dx, weight, weight, nullptr,
+      nullptr, partial, B * S, S, (int)H, kBwdRows, eps);
+  if (int rc = check_launch("head_norm_bwd")) return rc;
+  reduce_partials_kernel<<<1, 1024, 0, st>>>(partial, nchunk, kHd, dweight, dweight);
+  return check_launch("head_norm_bwd reduce");
+}

@@ -1,0 +1,222 @@
+/*
+ * anima_attn.h — C ABI of the MI355X (gfx950) DiT attention path.
+ *
+ * One shared library, libanima_attn.so, holds every kernel of the path:
+ * the QK-RMSNorm + 3D-RoPE prologue, per-head RMSNorm of cross-attention
+ * queries, the non-causal flash-attention forward (self, and key-length
+ * masked cross-attention with an optional fused padding correction), the
+ * flash-attention backward, and the padding-correction kernels on their own.
+ *
+ * Conventions shared by every entry point:
+ *   - Tensors are device pointers. Attention tensors are [B, S, H, hd]
+ *     ("BSHD") with the head-dim stride fixed to 1 and the other three
+ *     strides passed in elements (int64). Prologue tensors are contiguous.
+ *   - `stream` is a hipStream_t passed as void* (NULL = the null stream).
+ *     Every call is asynchronous on that stream; no call synchronises the
+ *     host and none allocates or frees device memory: outputs and
+ *     workspaces are allocated by the caller.
+ *   - Return codes: AA_OK (0); AA_EINVAL (-1) for a bad argument (null
+ *     pointer, inconsistent shape, misaligned pointer or stride);
+ *     AA_EUNSUPPORTED (-2) for a shape or dtype the kernels do not
+ *     implement; AA_EHIP (-3) when a HIP launch reports an error.
+ *     aa_last_error() returns the calling thread's last message.
+ *   - Only dtype AA_DTYPE_BF16 is implemented for activations; weights,
+ *     rotary tables, LSE and padding logs are float32; key lengths int32.
+ *   - hd (head_dim) must be 128.
+ *
+ * The reference (anima-flat) has no C FFI of its own: its path is Python
+ * calling FlashAttention-4 (CuTe DSL) and Triton kernels. Each entry point
+ * below names the reference function (file:line under src/) whose work it
+ * replaces; the Python host layer in anima-flat_amd/ keeps those functions'
+ * signatures and calls these entry points through ctypes.
+ */
+#ifndef ANIMA_ATTN_H
+#define ANIMA_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define AA_ABI_VERSION 1
+
+enum {
+  AA_OK = 0,
+  AA_EINVAL = -1,
+  AA_EUNSUPPORTED = -2,
+  AA_EHIP = -3,
+};
+
+enum {
+  AA_DTYPE_BF16 = 0,
+  AA_DTYPE_FP16 = 1, /* reserved: rejected with AA_EUNSUPPORTED */
+};
+
+/* ABI version of the loaded library (AA_ABI_VERSION when built from this header). */
+int aa_abi_version(void);
+
+/* Last error message of the calling thread ("" if none). Valid until the next call. */
+const char* aa_last_error(void);
+
+/* ------------------------------------------------------------------------ */
+/* Prologue                                                                  */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * Per-head RMSNorm of the q and k sections of a fused QKV projection output,
+ * rounded to the activation dtype, then rotate-half RoPE; optional V copy.
+ *   qkv [B, S, 3*H*hd] contiguous; q, k [B, S, H, hd] contiguous outputs;
+ *   v   [B, S, H, hd] output or NULL (NULL: V is not copied);
+ *   q_weight, k_weight [hd] float32; cos, sin [S, hd/2] float32;
+ *   position of token (b, s) is s.
+ * Replaces: src/kernels/rope.py:175-193 (_qkv_norm_rope, v == NULL) and
+ *           src/kernels/rope.py:504-523 (_qkv_norm_rope_v, v != NULL),
+ *           kernel src/kernels/rope.py:61-143.
+ */
+int aa_qkv_norm_rope_fwd(const void* qkv, void* q, void* k, void* v,
+                         const float* q_weight, const float* k_weight,
+                         const float* cos, const float* sin,
+                         int64_t B, int64_t S, int64_t H, int64_t hd,
+                         float eps, int dtype, void* stream);
+
+/*
+ * Per-head RMSNorm: x [B, S, H*hd] contiguous -> y [B, S, H, hd] contiguous.
+ * Replaces: src/kernels/rope.py:203-212 (_head_norm), kernel rope.py:146-172.
+ */
+int aa_head_norm_fwd(const void* x, void* y, const float* weight,
+                     int64_t B, int64_t S, int64_t H, int64_t hd,
+                     float eps, int dtype, void* stream);
+
+/* Bytes of workspace aa_qkv_norm_rope_bwd needs (weight-grad partials). */
+size_t aa_qkv_norm_rope_bwd_workspace(int64_t B, int64_t S, int64_t H, int64_t hd);
+
+/*
+ * Backward of aa_qkv_norm_rope_fwd (with V copied):
+ *   dq, dk, dv [B, S, H, hd] contiguous -> dqkv [B, S, 3*H*hd],
+ *   dq_weight, dk_weight [hd] float32 (sums over every token and head).
+ * The weight-gradient reduction runs in a fixed order (deterministic).
+ * Replaces: src/kernels/rope.py:540-577 (_qkv_norm_rope_bwd),
+ *           kernel rope.py:277-383, helper rope.py:223-274.
+ */
+int aa_qkv_norm_rope_bwd(const void* qkv, const void* dq, const void* dk,
+                         const void* dv, void* dqkv,
+                         const float* q_weight, const float* k_weight,
+                         const float* cos, const float* sin,
+                         float* dq_weight, float* dk_weight,
+                         void* workspace, size_t workspace_bytes,
+                         int64_t B, int64_t S, int64_t H, int64_t hd,
+                         float eps, int dtype, void* stream);
+
+/* Bytes of workspace aa_head_norm_bwd needs. */
+size_t aa_head_norm_bwd_workspace(int64_t B, int64_t S, int64_t H, int64_t hd);
+
+/*
+ * Backward of aa_head_norm_fwd: x, dy [B, S, H*hd] -> dx [B, S, H*hd],
+ * dweight [hd] float32.
+ * Replaces: src/kernels/rope.py:443-471 (_head_norm_bwd), kernel rope.py:386-436.
+ */
+int aa_head_norm_bwd(const void* x, const void* dy, void* dx,
+                     const float* weight, float* dweight,
+                     void* workspace, size_t workspace_bytes,
+                     int64_t B, int64_t S, int64_t H, int64_t hd,
+                     float eps, int dtype, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Flash attention                                                           */
+/* ------------------------------------------------------------------------ */
+
+typedef struct aa_attn_fwd_args {
+  const void* q;        /* [B, Sq, H, hd] */
+  const void* k;        /* [B, Sk, H, hd] */
+  const void* v;        /* [B, Sk, H, hd] */
+  void* out;            /* [B, Sq, H, hd] */
+  float* lse;           /* [B, H, Sq] contiguous natural-log LSE, or NULL */
+  const int32_t* seqused_k; /* [B] keys attended per batch item, or NULL (all Sk) */
+  const float* ln_pad;  /* [B] log(#padding keys) for the fused padding
+                           correction out *= 1/(1+exp(ln_pad-lse)), or NULL */
+  int64_t q_stride[3];  /* batch, seq, head strides in elements */
+  int64_t k_stride[3];
+  int64_t v_stride[3];
+  int64_t out_stride[3];
+  int64_t B, Sq, Sk, H, hd;
+  float softmax_scale;  /* usually 1/sqrt(hd) */
+  int dtype;
+} aa_attn_fwd_args;
+
+/*
+ * out = softmax(q k^T * softmax_scale) v, non-causal, per (batch, head);
+ * keys j >= seqused_k[b] are excluded when seqused_k != NULL; lse is the
+ * natural-log row log-sum-exp of the scaled scores over the attended keys.
+ * Replaces: src/attention.py:43-53 (anima_flat::fa_fwd),
+ *           src/attention.py:63-66 (anima_flat::fa_fwd_nolse),
+ *           src/attention.py:74-81 (anima_flat::fa_fwd_k), and with
+ *           ln_pad != NULL also the ctx_scale pass of
+ *           src/attention.py:156-180 (cross_attention_trimmed).
+ */
+int aa_attn_fwd(const aa_attn_fwd_args* args, void* stream);
+
+typedef struct aa_attn_bwd_args {
+  const void* dout;     /* [B, Sq, H, hd] */
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* out;
+  const float* lse;     /* [B, H, Sq] contiguous, from aa_attn_fwd */
+  void* dq;             /* [B, Sq, H, hd] */
+  void* dk;             /* [B, Sk, H, hd] */
+  void* dv;             /* [B, Sk, H, hd] */
+  int64_t dout_stride[3];
+  int64_t q_stride[3];
+  int64_t k_stride[3];
+  int64_t v_stride[3];
+  int64_t out_stride[3];
+  int64_t dq_stride[3];
+  int64_t dk_stride[3];
+  int64_t dv_stride[3];
+  int64_t B, Sq, Sk, H, hd;
+  float softmax_scale;
+  int dtype;
+} aa_attn_bwd_args;
+
+/* Bytes of workspace aa_attn_bwd needs (per-row dO.O dot products). */
+size_t aa_attn_bwd_workspace(int64_t B, int64_t Sq, int64_t Sk, int64_t H, int64_t hd);
+
+/*
+ * dq, dk, dv of aa_attn_fwd (no key mask), softmax recomputed from lse.
+ * Deterministic: no atomics, every sum runs in a fixed order.
+ * Replaces: src/attention.py:91-103 (anima_flat::fa_bwd), reached through
+ *           the autograd registration at src/attention.py:111-123.
+ */
+int aa_attn_bwd(const aa_attn_bwd_args* args, void* workspace,
+                size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Padding correction of trimmed cross-attention                             */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * y = out * 1/(1 + exp(ln_pad[b] - lse[b, h, s])); out, y [B, S, H, hd]
+ * contiguous, lse [B, H, S], ln_pad [B].
+ * Replaces: src/kernels/ctx_scale.py:39-55 (kernel ctx_scale.py:8-36).
+ */
+int aa_ctx_scale_fwd(const void* out, const float* lse, const float* ln_pad,
+                     void* y, int64_t B, int64_t S, int64_t H, int64_t hd,
+                     int dtype, void* stream);
+
+/*
+ * dout = dy * g, dlse[b,h,s] = sum_d(dy * out) * g * (1 - g) with
+ * g = 1/(1 + exp(ln_pad[b] - lse[b,h,s])).
+ * Replaces: src/kernels/ctx_scale.py:98-117 (kernel ctx_scale.py:63-95).
+ */
+int aa_ctx_scale_bwd(const void* out, const float* lse, const float* ln_pad,
+                     const void* dy, void* dout, float* dlse,
+                     int64_t B, int64_t S, int64_t H, int64_t hd,
+                     int dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ANIMA_ATTN_H */
