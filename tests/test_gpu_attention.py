@@ -19,6 +19,11 @@ pytestmark = pytest.mark.gpu
 
 BF = torch.bfloat16
 
+# The kernel's LSE is the log of the sum of the bf16-rounded probabilities
+# that weight V (so the output is exactly normalised); it differs from the
+# fp32 logsumexp by ~2^-9 / sqrt(#keys) relative in the sum, i.e. < 1e-3 in lse.
+LSE_TOL = dict(max_abs=2e-3, rel_l2=2e-4)
+
 
 def _qkv(B, Sq, Sk, H, seed, hd=128):
     g = torch.Generator().manual_seed(seed)
@@ -59,7 +64,7 @@ def test_attention_forward_lse(pkg):
     eo, el = ref.attention_lse(q, k, v)
     assert lse.shape == (2, 3, 300) and lse.dtype == torch.float32
     parity(out, eo, name="fa_fwd out")
-    parity(lse, el, max_abs=1e-3, rel_l2=1e-5, name="fa_fwd lse")
+    parity(lse, el, **LSE_TOL, name="fa_fwd lse")
 
 
 def test_attention_config2_full(pkg):
@@ -106,7 +111,7 @@ def test_masked_forward(pkg, lens):
     torch.cuda.synchronize()
     eo, el = ref.attention_lse(q, k, v, seq)
     parity(out, eo, name=f"fa_fwd_k out {lens}")
-    parity(lse, el, max_abs=1e-3, rel_l2=1e-5, name=f"fa_fwd_k lse {lens}")
+    parity(lse, el, **LSE_TOL, name=f"fa_fwd_k lse {lens}")
     # Equals plain attention over the first len keys.
     for b, n in enumerate(lens):
         parity(out[b : b + 1], ref.attention_sdpa(q[b : b + 1], k[b : b + 1, :n], v[b : b + 1, :n]),
@@ -155,7 +160,7 @@ def test_config3_masked_full(pkg):
     parity(qd, q, name="config3 head_norm")
     eo, el = ref.attention_lse(q, k, v, lens)
     parity(out, eo, name="config3 masked out")
-    parity(lse, el, max_abs=1e-3, rel_l2=1e-5, name="config3 masked lse")
+    parity(lse, el, **LSE_TOL, name="config3 masked lse")
 
 
 @pytest.mark.parametrize(
