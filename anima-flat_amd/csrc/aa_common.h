@@ -76,6 +76,14 @@ __device__ __forceinline__ float pair_sum(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// max(a, b, c) in one v_max3_f32. fmaxf would first canonicalise its inputs
+// (IEEE NaN quieting, an extra v_max_f32 each); the path's scores hold no NaN.
+__device__ __forceinline__ float max3f(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
 // Sum over aligned groups of `width` lanes (width a power of two <= 64).
 template <int WIDTH>
 __device__ __forceinline__ float group_sum(float x) {

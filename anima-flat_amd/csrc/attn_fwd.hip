@@ -2,10 +2,11 @@
 // for gfx950 (CDNA4): v_mfma_f32_32x32x16_bf16 for both products.
 //
 // Work decomposition
-//   One workgroup = NW waves = NW*32 queries of one (batch, head). Each wave
+//   One workgroup = 8 waves = 256 queries of one (batch, head). Each wave
 //   owns 32 queries for the whole kernel; K/V tiles of 64 keys are streamed
-//   into LDS and shared by the NW waves. Two LDS stages: the DMA of tile t+1
-//   runs while tile t is consumed.
+//   into a 3-stage LDS ring and shared by the 8 waves. The waves run in two
+//   phase-shifted groups so that MFMA and softmax work overlap on every SIMD
+//   (schedule at the kernel).
 //
 // Transposed formulation (per wave, per 64-key tile)
 //   S^T = K Q^T   : A = K rows from LDS (32 keys x 16 d per MFMA),
@@ -19,13 +20,12 @@
 //   output rescale is a per-lane scalar multiply.
 //
 // K/V staging: global_load_lds_dwordx4 (DMA, no registers). A DMA instruction
-//   writes 64 lanes x 16 B contiguously, i.e. 4 rows of 256 B, so rows are not
-//   padded; bank conflicts (64 banks of 4 B) are avoided by XOR-swizzling the
-//   16-byte chunks of each row instead: chunk c of row r is stored at
-//   c ^ (r & 15) for K (the MFMA A reads hit 16 different rows per 16 lanes)
-//   and at c ^ 4*(r & 3) for V (a transposed read covers 4 rows x 64 B per
-//   32 lanes). The lane picks which global chunk it fetches so that the LDS
-//   side stays contiguous.
+//   writes 64 lanes x 16 B contiguously (1 KB), so rows cannot be padded;
+//   instead the tile is stored as 256-byte slices of (16-row group, 16-byte
+//   chunk), with an XOR on the slot for V, so that both operand reads are
+//   free of bank conflicts on the 64 banks of 4 B (layout at the DMA code).
+//   The lane picks which global row/chunk it fetches so that the LDS side
+//   stays contiguous.
 //
 // Transposed read (ds_read_b64_tr_b16): within each group of 16 lanes, lane i
 //   receives element (i & 3) of the 4 b16 values addressed by lanes
@@ -48,6 +48,7 @@
 //   64 accumulator registers) runs only a few times per row. The row sum is
 //   taken over the bf16-rounded P that feeds the MFMA, with v_dot2c_f32_bf16.
 #include <cmath>
+#include <cstdlib>
 #include <type_traits>
 
 #include "aa_common.h"
@@ -71,9 +72,57 @@ struct FwdParams {
   int64_t ks0, ks1, ks2;
   int64_t vs0, vs1, vs2;
   int64_t os0, os1, os2;
-  int H, Sq, Sk, nqblk, total_blocks;
+  const bf16* vt;  // V repacked by vt_pack_kernel: [B][H][ntk][8192]
+  int H, Sq, Sk, nqblk, total_blocks, ntk;
   float c;  // softmax_scale * log2(e)
 };
+
+// V^T tile format (one 64-key tile = 8192 elements, 16 KB), the exact LDS
+// image the PV operand reads want:
+//   element (d, key) at (d >> 4) * 1024 + c' * 128 + (d & 15) * 8 + e,
+// where the tile's keys are taken in 16-key chunks c4 and, within a chunk,
+// in the order that matches the P^T accumulator layout: c' = 2 c4 + h holds
+// keys 16 c4 + 4 h + {0..3} (e = 0..3) and 16 c4 + 8 + 4 h + {0..3} (e = 4..7).
+// A wave's 16-byte read for (dt, c4) is then lane li, h = lane / 32:
+//   (li >> 4) * 1024 + h * 128 + (li & 15) * 8 + 2048 dt + 256 c4,
+// 16 consecutive 16-byte slots per 16 lanes: no bank conflicts.
+__device__ __forceinline__ int vt_key(int cp, int e) {
+  return 16 * (cp >> 1) + 8 * ((e >> 2) & 1) + 4 * (cp & 1) + (e & 3);
+}
+
+// One workgroup per (tile, head, batch): V rows [64 t, 64 t + 64) into LDS
+// (coalesced 16-byte loads, zero past Sk), then gathered into the V^T tile
+// format and written out with coalesced 16-byte stores.
+__global__ __launch_bounds__(256) void vt_pack_kernel(const bf16* __restrict__ v, int64_t vs0,
+                                                      int64_t vs1, int64_t vs2, int Sk, int H,
+                                                      int ntk, bf16* __restrict__ vt) {
+  constexpr int kRow = 128 + 8;  // padded LDS row (elements)
+  __shared__ __attribute__((aligned(16))) bf16 tile[64 * kRow];
+  const int t = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x;
+  const bf16* src = v + b * vs0 + h * vs2;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int id = tid + 256 * i;
+    const int row = id >> 4, dc = id & 15;
+    const int key = 64 * t + row;
+    u32x4 w = {0u, 0u, 0u, 0u};
+    if (key < Sk) w = ld16(src + (int64_t)key * vs1 + 8 * dc);
+    st16(tile + row * kRow + 8 * dc, w);
+  }
+  __syncthreads();
+  bf16* dst = vt + (((int64_t)b * H + h) * ntk + t) * 8192;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int oi = tid + 256 * i;  // 16-byte output chunk, in output order
+    const int d = 16 * (oi >> 7) + (oi & 15);
+    const int cp = (oi >> 4) & 7;
+    bf16x8 w;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) w[e] = tile[vt_key(cp, e) * kRow + d];
+    *reinterpret_cast<bf16x8*>(dst + 8 * oi) = w;
+  }
+}
 
 typedef __attribute__((address_space(3))) void lds_void;
 typedef short s16x4 __attribute__((ext_vector_type(4)));
@@ -94,15 +143,37 @@ __device__ __forceinline__ s16x4 lds_read_tr(const bf16* p) {
 
 __device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-template <int NW>
-__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
+// 16 bytes per lane from global memory straight into LDS at
+// lds_base + 16 * lane (global_load_lds_dwordx4; M0 holds the LDS base).
+// Issued as inline asm so the compiler does not treat every later LDS read as
+// possibly depending on this write: completion is tracked by wait_dma() and
+// the workgroup barrier that follows it.
+__device__ __forceinline__ void dma16(const void* src, const void* lds_base) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void*)lds_base);
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0)
+               : "memory", "m0");
+}
+
+constexpr int kWaves = 8;    // two groups of 4, one wave of each group per SIMD
+constexpr int kDmaWaves = 4; // group A issues every DMA
+constexpr int kStages = 3;   // K/V ring depth
+constexpr int kQPerWg = kWaves * 32;
+
+// Phase-shifted ("ping-pong") schedule. Waves 0-3 (group A) and 4-7 (group B)
+// run the same per-tile work, one phase apart:
+//   M(j): O^T += V_{j-1}^T P_{j-1}^T (16 MFMA) and S_j^T = K_j Q^T (16 MFMA)
+//   X(j): softmax of S_j -> P_j (exp, max, sums, rare rescale)
+//   phase 2j  : A runs M(j), B runs X(j-1)
+//   phase 2j+1: A runs X(j), B runs M(j)
+// with a workgroup barrier between phases. Waves w and w+4 share a SIMD, so
+// on every SIMD one wave is in an MFMA block while its partner is in a VALU
+// block and the matrix and vector pipes overlap. Tile j sits in stage j % 3;
+// its DMA is issued at phase 2j-2 and complete (wait + barrier) by the end
+// of phase 2j-1; its K is read in phases 2j, 2j+1 and its V in 2j+2, 2j+3.
+__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_fwd_kernel(FwdParams p) {
-  static_assert(NW == 4 || NW == 8, "4 or 8 waves per workgroup");
-  constexpr int kDmaPerWave = 16 / NW;  // 1 KB DMA instructions per wave per tile (K and V each)
-  __shared__ __attribute__((aligned(1024))) bf16 k_lds0[kTileElems];
-  __shared__ __attribute__((aligned(1024))) bf16 k_lds1[kTileElems];
-  __shared__ __attribute__((aligned(1024))) bf16 v_lds0[kTileElems];
-  __shared__ __attribute__((aligned(1024))) bf16 v_lds1[kTileElems];
+  constexpr int kDmaPerWave = 16 / kDmaWaves;  // 1 KB DMA blocks per group-A wave per tile, K and V each
+  __shared__ __attribute__((aligned(1024))) bf16 kv_lds[kStages][2][kTileElems];
 
   // Block -> (batch, head, query block). Workgroups are dispatched round-robin
   // over the 8 XCDs; remap so each XCD gets a contiguous range of logical
@@ -118,6 +189,7 @@ void attn_fwd_kernel(FwdParams p) {
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool group_a = wave < 4;
   const int lane = tid & 63;
   const int li = lane & 31;
   const int hh = lane >> 5;
@@ -126,7 +198,7 @@ void attn_fwd_kernel(FwdParams p) {
   const int ntiles = klen > 0 ? (klen + kBN - 1) / kBN : 0;
 
   // Q^T operand: lane holds Q[query li][16*kk + 8*hh + 0..7] for kk = 0..7.
-  const int qrow = qblk * (NW * 32) + wave * 32 + li;
+  const int qrow = qblk * kQPerWg + wave * 32 + li;
   bf16x8 qreg[8];
   {
     const bf16* qp = p.q + b * p.qs0 + h * p.qs2 + (int64_t)qrow * p.qs1 + 8 * hh;
@@ -141,40 +213,50 @@ void attn_fwd_kernel(FwdParams p) {
   const bf16* kp = p.k + b * p.ks0 + h * p.ks2;
   const bf16* vp = p.v + b * p.vs0 + h * p.vs2;
 
-  // DMA of tile t into (kd, vd): this wave fills 1 KB blocks wave*kDmaPerWave + i
-  // (rows 4*blk .. 4*blk+3). Rows past klen re-read row klen-1 (finite data;
-  // their scores are masked).
-  auto issue_tile = [&](int t, bf16* kd, bf16* vd) {
+  // LDS tile layout (elements): row r, 16-byte chunk c of a 64 x 128 tile at
+  //   (r >> 4) * 2048 + c * 128 + slot(r, c) * 8, one 256-byte slice per
+  //   (16-row group, chunk). K: slot = r & 15 (the A-operand read of 16 lanes
+  //   covers 16 consecutive slots). V: slot = (r & 15) ^ 4 (c & 3) (a
+  //   transposed read of 32 lanes covers 4 rows x 4 chunks = 16 slots).
+  // A DMA instruction fills 1 KB = one 16-row group x 4 chunks; lane l writes
+  // slot l & 15 of chunk 4 (blk & 3) + (l >> 4), so it fetches row
+  // 16 (blk >> 2) + slot^-1 from global memory. Offsets are one per-lane base
+  // plus 32 elements per further block of the same wave.
+  const int b0 = wave * kDmaPerWave;
+  const int l15 = lane & 15, lq = lane >> 4;
+  const int dma_krow = 16 * (b0 >> 2) + l15;
+  const int dma_chunk0 = 4 * (b0 & 3) + lq;
+  const int dma_k = dma_krow * (int)p.ks1 + 8 * dma_chunk0;
+  // Rows past klen (last tile only) re-read row klen-1: finite data whose
+  // scores are masked to -inf, so their P is 0. V^T tiles come pre-packed and
+  // are copied linearly (16 KB: block b of the tile at 512 b elements).
+  const bf16* vtp = p.vt + ((int64_t)b * p.H + h) * p.ntk * 8192 + (b0 * 512 + lane * 8);
+  auto issue_tile = [&](int t) {
+    bf16* kd = kv_lds[t % kStages][0];
+    bf16* vd = kv_lds[t % kStages][1];
     const int kb = t * kBN;
-    const int slot = lane & 15;
+    const bf16* vsrc = vtp + (int64_t)t * 8192;
 #pragma unroll
-    for (int i = 0; i < kDmaPerWave; ++i) {
-      const int blk = wave * kDmaPerWave + i;
-      const int row = 4 * blk + (lane >> 4);
-      const int src = min(kb + row, klen - 1);
-      const bf16* gk = kp + (int64_t)src * p.ks1 + 8 * (slot ^ (row & 15));
-      const bf16* gv = vp + (int64_t)src * p.vs1 + 8 * (slot ^ (4 * (row & 3)));
-      __builtin_amdgcn_global_load_lds(gk, to_lds(kd + blk * 512), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(gv, to_lds(vd + blk * 512), 16, 0, 0);
+    for (int i = 0; i < kDmaPerWave; ++i) dma16(vsrc + 512 * i, vd + (b0 + i) * 512);
+    if (kb + kBN <= klen) {
+      const bf16* kt = kp + (int64_t)kb * p.ks1 + dma_k;
+#pragma unroll
+      for (int i = 0; i < kDmaPerWave; ++i) dma16(kt + 32 * i, kd + (b0 + i) * 512);
+    } else {
+      const int krow = min(kb + dma_krow, klen - 1);
+#pragma unroll
+      for (int i = 0; i < kDmaPerWave; ++i) {
+        const int chunk = dma_chunk0 + 4 * i;
+        dma16(kp + (int64_t)krow * p.ks1 + 8 * chunk, kd + (b0 + i) * 512);
+      }
     }
   };
 
-  // Per-lane LDS read offsets (elements). K operand (kt, kk): row 32kt + li,
-  // logical chunk 2kk + hh stored at (2kk + hh) ^ (li & 15).
-  int k_off[8];
-#pragma unroll
-  for (int kk = 0; kk < 8; ++kk) k_off[kk] = li * kD + 8 * ((2 * kk + hh) ^ (li & 15));
-  // V^T operand (dt, c4, half): source lane s = lane & 15 of group g = lane >> 4
-  // reads 4 d at row 16*c4 + 4*(g>>1) + 8*half + (s>>2), d = 32dt + 16(g&1) + 4(s&3).
-  const int g = lane >> 4, s = lane & 15;
-  const int vrow = 4 * (g >> 1) + (s >> 2);
-  int v_off[4];
-#pragma unroll
-  for (int dt = 0; dt < 4; ++dt) {
-    const int dcol = 32 * dt + 16 * (g & 1) + 4 * (s & 3);
-    const int chunk = (dcol >> 3) ^ (4 * (vrow & 3));
-    v_off[dt] = vrow * kD + 8 * chunk + (dcol & 7);
-  }
+  // Per-lane LDS read bases (elements). K operand (kt, kk): row 32kt + li,
+  // chunk 2kk + hh -> k_rd + 4096 kt + 256 kk.
+  const int k_rd = (li >> 4) * 2048 + (li & 15) * 8 + hh * 128;
+  // V^T operand (dt, c4): v_rd + 2048 dt + 256 c4 (tile format above).
+  const int v_rd = (li >> 4) * 1024 + hh * 128 + (li & 15) * 8;
 
   f32x16 o[4];
 #pragma unroll
@@ -188,26 +270,62 @@ void attn_fwd_kernel(FwdParams p) {
   const float c = p.c;
   const float thr_raw = kRescaleThreshold / c;
   const bf16x2 ones = {(bf16)1.0f, (bf16)1.0f};
+  f32x16 s0, s1;  // S^T of the tile between its M and X blocks
+  bf16x8 pb[4];   // P^T of the tile between its X block and the next M block
 
-  // One 64-key tile: S^T, softmax, O^T += V^T P^T. MASK excludes keys >= klen
-  // (only the last tile of a row can need it).
-  auto process = [&](const bf16* ks, const bf16* vs, int kb, auto mask_tag) {
-    constexpr bool MASK = decltype(mask_tag)::value;
-    // S^T = K Q^T: two independent 32-key accumulator chains.
-    f32x16 s0, s1;
+  // M block: up to 32 MFMAs in one unrolled stream, fed by a queue of LDS
+  // operands read kPrefetch MFMAs ahead (sched_barrier fences pin the order):
+  //   ops 0-15 : O^T += V^T P^T of tile tv, op = 4 c4 + dt (A operand: one
+  //              16-byte read of the V^T tile)
+  //   ops 16-31: S^T = K Q^T of tile tk, op = 16 + 2 kk + kt (A operand: one
+  //              16-byte read of the K tile; two accumulator chains s0, s1)
+  // PV / QK select which half runs (the first tile has no PV, the tail no QK).
+  constexpr int kPrefetch = 12;
+  auto mblock = [&](int tv, int tk, auto pv_tag, auto qk_tag) {
+    constexpr bool PV = decltype(pv_tag)::value;
+    constexpr bool QK = decltype(qk_tag)::value;
+    constexpr int first = PV ? 0 : 16;
+    constexpr int last = QK ? 32 : 16;
+    const bf16* vs = kv_lds[tv % kStages][1];
+    const bf16* ks = kv_lds[tk % kStages][0];
+    if constexpr (QK) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      s0[r] = 0.f;
-      s1[r] = 0.f;
+      for (int r = 0; r < 16; ++r) {
+        s0[r] = 0.f;
+        s1[r] = 0.f;
+      }
     }
+    bf16x8 q_ops[kPrefetch];
+    auto load_op = [&](int op) -> bf16x8 {
+      if (op < 16) {
+        const int c4 = op >> 2, dt = op & 3;
+        return *reinterpret_cast<const bf16x8*>(vs + v_rd + 2048 * dt + 256 * c4);
+      }
+      const int kk = (op - 16) >> 1, kt = (op - 16) & 1;
+      return *reinterpret_cast<const bf16x8*>(ks + k_rd + 4096 * kt + 256 * kk);
+    };
+    auto run_op = [&](int op, bf16x8 a) {
+      if (op < 16) {
+        const int c4 = op >> 2, dt = op & 3;
+        o[dt] = mfma32(a, pb[c4], o[dt]);
+      } else {
+        const int kk = (op - 16) >> 1, kt = (op - 16) & 1;
+        if (kt == 0) s0 = mfma32(a, qreg[kk], s0);
+        else s1 = mfma32(a, qreg[kk], s1);
+      }
+    };
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk) {
-      const bf16x8 x0 = *reinterpret_cast<const bf16x8*>(ks + k_off[kk]);
-      const bf16x8 x1 = *reinterpret_cast<const bf16x8*>(ks + 32 * kD + k_off[kk]);
-      s0 = mfma32(x0, qreg[kk], s0);
-      s1 = mfma32(x1, qreg[kk], s1);
+    for (int i = first; i < last + kPrefetch; ++i) {
+      // Consume slot (i - first) % kPrefetch before refilling it.
+      if (i - kPrefetch >= first) run_op(i - kPrefetch, q_ops[(i - kPrefetch - first) % kPrefetch]);
+      if (i < last) q_ops[(i - first) % kPrefetch] = load_op(i);
+      __builtin_amdgcn_sched_barrier(0);
     }
-    if constexpr (MASK) {
+  };
+  // Softmax of tile t: mask (last tile only), row max, lazy rescale, P, sums.
+  auto softmax = [&](int t) {
+    const int kb = t * kBN;
+    if (kb + kBN > klen) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int key = kb + 8 * (r >> 2) + 4 * hh + (r & 3);
@@ -215,10 +333,15 @@ void attn_fwd_kernel(FwdParams p) {
         if (key + 32 >= klen) s1[r] = -INFINITY;
       }
     }
-    // Row max of the raw scores, then over the lane pair.
-    float mt = fmaxf(s0[0], s1[0]);
+    // Row max of the raw scores (two v_max3 chains), then over the lane pair.
+    float ma = max3f(s0[0], s1[0], s0[1]);
+    float mb = max3f(s1[1], s0[2], s1[2]);
 #pragma unroll
-    for (int r = 1; r < 16; ++r) mt = fmaxf(mt, fmaxf(s0[r], s1[r]));
+    for (int r = 3; r < 15; r += 2) {
+      ma = max3f(ma, s0[r], s1[r]);
+      mb = max3f(mb, s0[r + 1], s1[r + 1]);
+    }
+    float mt = max3f(ma, mb, fmaxf(s0[15], s1[15]));
     mt = pair_max(mt);
 
     const bool need = mt > m_raw + thr_raw;
@@ -236,7 +359,6 @@ void attn_fwd_kernel(FwdParams p) {
 
     // P^T = exp2(s c - m c) in bf16 as four 16-key B operands.
     const float mc = m_raw * c;
-    bf16x8 pb[4];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       pb[0][i] = (bf16)fast_exp2(fmaf(s0[i], c, -mc));
@@ -253,54 +375,37 @@ void attn_fwd_kernel(FwdParams p) {
         l4[c4] = __builtin_amdgcn_fdot2_f32_bf16(pair, ones, l4[c4], false);
       }
     }
-
-    // O^T += V^T P^T: A operand from two transposed reads (keys 4h.. and 8+4h..).
-#pragma unroll
-    for (int c4 = 0; c4 < 4; ++c4) {
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt) {
-        const bf16* base = vs + 16 * c4 * kD + v_off[dt];
-        const s16x4 lo = lds_read_tr(base);
-        const s16x4 hi = lds_read_tr(base + 8 * kD);
-        const s16x8 both = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-        o[dt] = mfma32(__builtin_bit_cast(bf16x8, both), pb[c4], o[dt]);
-      }
-    }
   };
 
-  // Main loop over full tiles, unrolled by two so that each half reads one
-  // statically known LDS stage while the DMA fills the other.
-  const int nfull = klen / kBN;  // tiles whose 64 keys are all valid
-  if (ntiles > 0) {
-    issue_tile(0, k_lds0, v_lds0);
+  // Both groups run the same instruction stream, M(m) | barrier | X(m) |
+  // barrier; group B executes one extra barrier first (group A one extra at
+  // the end), which shifts B by exactly one phase. Only group A issues and
+  // waits for the DMA: tile m+1 at the start of its M(m), complete before the
+  // barrier that ends its X(m); the barriers order it for group B.
+  if (group_a && ntiles > 0) {
+    issue_tile(0);
     wait_dma();
   }
   __syncthreads();
-  int t = 0;
-  for (; t + 1 < nfull; t += 2) {
-    issue_tile(t + 1, k_lds1, v_lds1);
-    process(k_lds0, v_lds0, t * kBN, std::false_type{});
-    wait_dma();
+  if (!group_a) __syncthreads();
+  if (ntiles > 0) {
+    if (group_a && 1 < ntiles) issue_tile(1);
+    mblock(0, 0, std::false_type{}, std::true_type{});
     __syncthreads();
-    if (t + 2 < ntiles) issue_tile(t + 2, k_lds0, v_lds0);
-    process(k_lds1, v_lds1, (t + 1) * kBN, std::false_type{});
-    wait_dma();
+    softmax(0);
+    if (group_a) wait_dma();
     __syncthreads();
-  }
-  // At most two tiles remain: one full tile (odd nfull) and/or the partial
-  // tail; tile t sits in stage t & 1.
-  for (; t < ntiles; ++t) {
-    bf16* kc = (t & 1) ? k_lds1 : k_lds0;
-    bf16* vc = (t & 1) ? v_lds1 : v_lds0;
-    if (t + 1 < ntiles) issue_tile(t + 1, (t & 1) ? k_lds0 : k_lds1, (t & 1) ? v_lds0 : v_lds1);
-    if (t < nfull) {
-      process(kc, vc, t * kBN, std::false_type{});
-    } else {
-      process(kc, vc, t * kBN, std::true_type{});
+    for (int m = 1; m < ntiles; ++m) {
+      if (group_a && m + 1 < ntiles) issue_tile(m + 1);
+      mblock(m - 1, m, std::true_type{}, std::true_type{});
+      __syncthreads();
+      softmax(m);
+      if (group_a) wait_dma();
+      __syncthreads();
     }
-    wait_dma();
-    __syncthreads();
+    mblock(ntiles - 1, ntiles - 1, std::true_type{}, std::false_type{});
   }
+  if (group_a) __syncthreads();
 
   const float m_run = m_raw * c;
   const float l_run = (l4[0] + l4[1]) + (l4[2] + l4[3]);
@@ -334,6 +439,14 @@ static bool stride_ok(const int64_t* s) {
 
 using namespace aa;
 
+static int64_t vt_tiles(int64_t Sk) { return (Sk + kBN - 1) / kBN; }
+
+extern "C" size_t aa_attn_fwd_workspace(int64_t B, int64_t Sk, int64_t H, int64_t hd) {
+  (void)hd;
+  if (B <= 0 || Sk <= 0 || H <= 0) return 0;
+  return (size_t)(B * H * vt_tiles(Sk)) * kTileElems * sizeof(bf16);
+}
+
 extern "C" int aa_attn_fwd(const aa_attn_fwd_args* a, void* stream) {
   clear_error();
   if (!a) return fail(AA_EINVAL, "attn_fwd: null args");
@@ -353,8 +466,17 @@ extern "C" int aa_attn_fwd(const aa_attn_fwd_args* a, void* stream) {
   if (a->ln_pad && !a->seqused_k) return fail(AA_EINVAL, "attn_fwd: ln_pad needs seqused_k");
   if (!(a->softmax_scale > 0.f) || !std::isfinite(a->softmax_scale))
     return fail(AA_EINVAL, "attn_fwd: softmax_scale must be positive and finite");
+  // Per-lane DMA offsets within a 64-key tile are 32-bit.
+  if (std::llabs(a->k_stride[1]) >= (1 << 24) || std::llabs(a->v_stride[1]) >= (1 << 24))
+    return fail(AA_EUNSUPPORTED, "attn_fwd: key/value sequence stride must be < 2^24 elements");
 
-  constexpr int NW = 4;
+  const size_t ws_need = aa_attn_fwd_workspace(a->B, a->Sk, a->H, a->hd);
+  if (ws_need > 0 && (!a->workspace || a->workspace_bytes < ws_need))
+    return fail(AA_EINVAL, "attn_fwd: workspace too small");
+  if (ws_need > 0 && !aligned16(a->workspace))
+    return fail(AA_EINVAL, "attn_fwd: workspace must be 16-byte aligned");
+  if (vt_tiles(a->Sk) > 65535) return fail(AA_EUNSUPPORTED, "attn_fwd: Sk too large");
+
   FwdParams p;
   p.q = (const bf16*)a->q;
   p.k = (const bf16*)a->k;
@@ -370,11 +492,19 @@ extern "C" int aa_attn_fwd(const aa_attn_fwd_args* a, void* stream) {
   p.H = (int)a->H;
   p.Sq = (int)a->Sq;
   p.Sk = (int)a->Sk;
-  p.nqblk = (int)((a->Sq + NW * 32 - 1) / (NW * 32));
+  p.nqblk = (int)((a->Sq + kQPerWg - 1) / kQPerWg);
   const int64_t total = a->B * a->H * p.nqblk;
   if (total > 0x7fffffff) return fail(AA_EUNSUPPORTED, "attn_fwd: grid too large");
   p.total_blocks = (int)total;
   p.c = a->softmax_scale * kLog2e;
-  attn_fwd_kernel<NW><<<dim3((unsigned)total), NW * 64, 0, (hipStream_t)stream>>>(p);
+  p.ntk = (int)vt_tiles(a->Sk);
+  p.vt = (const bf16*)a->workspace;
+  hipStream_t st = (hipStream_t)stream;
+  if (a->Sk > 0) {
+    vt_pack_kernel<<<dim3((unsigned)p.ntk, (unsigned)a->H, (unsigned)a->B), 256, 0, st>>>(
+        p.v, p.vs0, p.vs1, p.vs2, p.Sk, p.H, p.ntk, (bf16*)a->workspace);
+    if (int rc = check_launch("attn_fwd vt_pack")) return rc;
+  }
+  attn_fwd_kernel<<<dim3((unsigned)total), kWaves * 64, 0, st>>>(p);
   return check_launch("attn_fwd");
 }

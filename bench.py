@@ -113,6 +113,12 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
+    ap.add_argument(
+        "--copy-calibration",
+        action="store_true",
+        help="also run one plain 256 MiB device copy (known bytes) so rocprofv3 FETCH_SIZE/"
+        "WRITE_SIZE can be scaled to bytes",
+    )
     args = ap.parse_args()
     if args.gpus != 1:
         print(
@@ -134,6 +140,13 @@ def main() -> int:
         q, k, v = pkg.qkv_norm_rope(p["qkv"], p["q_weight"], p["k_weight"], p["cos"], p["sin"], H, eps)
         fwd = torch.ops.anima_flat.fa_fwd_nolse
         wall_ms, dev_ms = time_launches(lambda: fwd(q, k, v), args.steps, args.warmup)
+    if args.copy_calibration:
+        src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     flops = attn_flops(B, H, S, S, d)
     value = flops / (wall_ms * 1e-3) / 1e12
     achieved = flops / (dev_ms * 1e-3) / 1e12

@@ -143,7 +143,13 @@ typedef struct aa_attn_fwd_args {
   int64_t B, Sq, Sk, H, hd;
   float softmax_scale;  /* usually 1/sqrt(hd) */
   int dtype;
+  void* workspace;      /* device scratch of aa_attn_fwd_workspace() bytes */
+  size_t workspace_bytes;
 } aa_attn_fwd_args;
+
+/* Bytes of device workspace aa_attn_fwd needs: V repacked as transposed
+ * 64-key tiles (B * H * ceil(Sk / 64) * 16 KiB). */
+size_t aa_attn_fwd_workspace(int64_t B, int64_t Sk, int64_t H, int64_t hd);
 
 /*
  * out = softmax(q k^T * softmax_scale) v, non-causal, per (batch, head);
