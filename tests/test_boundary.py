@@ -1,0 +1,207 @@
+"""CPU tests of the drop-in boundary: the C ABI library and the Python layer.
+
+No kernel runs here: the C-ABI calls below fail argument validation before any
+HIP call, and the Python ops are exercised through their fake (meta)
+implementations.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+import re
+import subprocess
+import sys
+from pathlib import Path
+
+import pytest
+import torch
+
+import __graft_entry__
+from oracle import attn_oracle as ref
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "anima_attn.h"
+
+
+@pytest.fixture(scope="module")
+def lib(pkg):
+    if not pkg._lib.LIB_PATH.exists():
+        pytest.skip("libanima_attn.so not built (run __graft_entry__.build())")
+    return pkg._lib.lib()
+
+
+def _declared_functions() -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(aa_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_entry_points():
+    names = _declared_functions()
+    for expected in (
+        "aa_abi_version",
+        "aa_last_error",
+        "aa_qkv_norm_rope_fwd",
+        "aa_qkv_norm_rope_bwd",
+        "aa_head_norm_fwd",
+        "aa_head_norm_bwd",
+        "aa_attn_fwd",
+        "aa_attn_fwd_workspace",
+        "aa_attn_bwd",
+        "aa_attn_bwd_workspace",
+        "aa_ctx_scale_fwd",
+        "aa_ctx_scale_bwd",
+    ):
+        assert expected in names
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in _declared_functions():
+        assert hasattr(lib, name), f"{name} missing from libanima_attn.so"
+    out = subprocess.run(["nm", "-D", "--defined-only", str(ROOT / "anima-flat_amd" / "libanima_attn.so")],
+                         capture_output=True, text=True, check=True).stdout
+    exported = set(re.findall(r"\bT (aa_[a-z0-9_]+)", out))
+    assert set(_declared_functions()) <= exported
+
+
+def test_python_binding_covers_the_header(pkg):
+    assert set(pkg._lib.EXPORTED) == set(_declared_functions())
+
+
+def test_abi_version(pkg, lib):
+    assert lib.aa_abi_version() == pkg._lib.ABI_VERSION
+
+
+def test_structs_match_header_field_order(pkg):
+    text = HEADER.read_text()
+    for struct, cls in (("aa_attn_fwd_args", pkg._lib.AttnFwdArgs), ("aa_attn_bwd_args", pkg._lib.AttnBwdArgs)):
+        body = re.search(r"typedef struct %s \{(.*?)\} %s;" % (struct, struct), text, re.S).group(1)
+        body = re.sub(r"/\*.*?\*/", "", body, flags=re.S)
+        types = {"const", "void", "float", "int", "int32_t", "int64_t", "size_t"}
+        fields = [tok.split("[")[0] for decl in body.split(";")
+                  for tok in re.findall(r"[A-Za-z_][A-Za-z0-9_]*(?:\[\d+\])?", decl)
+                  if tok.split("[")[0] not in types]
+        assert [f[0] for f in cls._fields_] == fields
+
+
+def test_workspace_sizes(lib):
+    assert lib.aa_attn_fwd_workspace(1, 4096, 16, 128) == 16 * 64 * 16384
+    assert lib.aa_attn_fwd_workspace(2, 77, 3, 128) == 2 * 3 * 2 * 16384
+    assert lib.aa_attn_fwd_workspace(0, 77, 3, 128) == 0
+    assert lib.aa_attn_bwd_workspace(2, 100, 77, 3, 128) == 2 * 3 * 100 * 4
+    assert lib.aa_qkv_norm_rope_bwd_workspace(1, 4096, 16, 128) == 256 * 2 * 128 * 4
+    assert lib.aa_head_norm_bwd_workspace(2, 9, 5, 128) == 2 * 128 * 4
+
+
+def test_invalid_arguments_fail_before_any_launch(pkg, lib):
+    L = pkg._lib
+    assert lib.aa_attn_fwd(None, None) == L.AA_EINVAL
+    assert "null args" in lib.aa_last_error().decode()
+    a = L.AttnFwdArgs()
+    a.B, a.Sq, a.Sk, a.H, a.hd, a.dtype, a.softmax_scale = 1, 4, 4, 1, 64, 0, 0.125
+    assert lib.aa_attn_fwd(ctypes.byref(a), None) == L.AA_EUNSUPPORTED
+    assert "head_dim" in lib.aa_last_error().decode()
+    a.hd, a.dtype = 128, 1
+    assert lib.aa_attn_fwd(ctypes.byref(a), None) == L.AA_EUNSUPPORTED
+    a.dtype = 0
+    assert lib.aa_attn_fwd(ctypes.byref(a), None) == L.AA_EINVAL  # null tensors
+    b = L.AttnBwdArgs()
+    assert lib.aa_attn_bwd(None, None, 0, None) == L.AA_EINVAL
+    b.B, b.Sq, b.Sk, b.H, b.hd, b.dtype = 1, 4, 4, 1, 128, 0
+    assert lib.aa_attn_bwd(ctypes.byref(b), None, 0, None) == L.AA_EINVAL
+    assert lib.aa_qkv_norm_rope_fwd(None, None, None, None, None, None, None, None, 1, 4, 2, 128, 1e-6, 0, None) == L.AA_EINVAL
+    assert lib.aa_head_norm_fwd(None, None, None, 1, 4, 2, 96, 1e-6, 0, None) == L.AA_EUNSUPPORTED
+    assert lib.aa_ctx_scale_fwd(None, None, None, None, 1, 4, 2, 128, 3, None) == L.AA_EUNSUPPORTED
+    with pytest.raises(ValueError):
+        L.check(L.AA_EINVAL, "x")
+    with pytest.raises(RuntimeError):
+        L.check(L.AA_EHIP, "x")
+
+
+def test_cpu_tensors_are_rejected(pkg):
+    q = torch.zeros(1, 4, 1, 128, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="CUDA tensors required"):
+        pkg.attention(q, q, q)
+    with pytest.raises(ValueError, match="CUDA tensors required"):
+        pkg.cross_attention_trimmed(q, q, q, torch.tensor([4], dtype=torch.int32), torch.tensor([0.0]))
+    qkv = torch.zeros(1, 4, 3 * 128, dtype=torch.bfloat16)
+    w = torch.ones(128)
+    cos = torch.ones(4, 64)
+    with pytest.raises(ValueError, match="CUDA tensors required"):
+        pkg.qkv_norm_rope(qkv, w, w, cos, cos, 1)
+    with pytest.raises(ValueError, match="CUDA tensors required"):
+        pkg.head_norm(torch.zeros(1, 4, 128, dtype=torch.bfloat16), w, 1)
+    with pytest.raises(ValueError, match="CUDA tensors required"):
+        pkg.ctx_scale(q, torch.zeros(1, 1, 4), torch.zeros(1))
+    assert pkg.use_fa4(q) is False
+
+
+def test_ops_are_registered_with_reference_names(pkg):
+    for name in ("fa_fwd", "fa_fwd_nolse", "fa_fwd_k", "fa_bwd", "qkv_norm_rope", "qkv_norm_rope_v",
+                 "qkv_norm_rope_bwd", "head_norm", "head_norm_bwd", "ctx_scale", "ctx_scale_bwd"):
+        assert hasattr(torch.ops.anima_flat, name), name
+
+
+def test_fake_shapes_on_meta_tensors(pkg):
+    B, Sq, Sk, H = 2, 40, 24, 3
+    q = torch.empty(B, Sq, H, 128, dtype=torch.bfloat16, device="meta")
+    k = torch.empty(B, Sk, H, 128, dtype=torch.bfloat16, device="meta")
+    out, lse = torch.ops.anima_flat.fa_fwd(q, k, k)
+    assert out.shape == q.shape and lse.shape == (B, H, Sq) and lse.dtype == torch.float32
+    assert torch.ops.anima_flat.fa_fwd_nolse(q, k, k).shape == q.shape
+    seq = torch.empty(B, dtype=torch.int32, device="meta")
+    out, lse = torch.ops.anima_flat.fa_fwd_k(q, k, k, seq)
+    assert out.shape == q.shape and lse.shape == (B, H, Sq)
+    dq, dk, dv = torch.ops.anima_flat.fa_bwd(q, q, k, k, q, lse)
+    assert dq.shape == q.shape and dk.shape == k.shape and dv.shape == k.shape
+    qkv = torch.empty(B, Sq, 3 * H * 128, dtype=torch.bfloat16, device="meta")
+    w = torch.empty(128, device="meta")
+    cos = torch.empty(Sq, 64, device="meta")
+    qq, kk = torch.ops.anima_flat.qkv_norm_rope(qkv, w, w, cos, cos, H, 1e-6)
+    assert qq.shape == kk.shape == (B, Sq, H, 128)
+    qq, kk, vv = torch.ops.anima_flat.qkv_norm_rope_v(qkv, w, w, cos, cos, H, 1e-6)
+    assert vv.shape == (B, Sq, H, 128)
+    x = torch.empty(B, Sq, H * 128, dtype=torch.bfloat16, device="meta")
+    assert torch.ops.anima_flat.head_norm(x, w, H, 1e-6).shape == (B, Sq, H, 128)
+    y = torch.ops.anima_flat.ctx_scale(q, lse, torch.empty(B, device="meta"))
+    assert y.shape == q.shape
+
+
+def test_rope_tables_bit_identical_to_oracle(pkg):
+    for h, w, scale in ((32, 32, (1.0, 1.0)), (64, 64, (4.0, 4.0)), (3, 5, (1.0, 1.0))):
+        c, s = pkg.rope_tables(h, w, 128, "cpu", scale)
+        rc, rs = ref.rope_tables(h, w, 128, scale)
+        assert torch.equal(c, rc) and torch.equal(s, rs)
+
+
+def test_trim_context_bookkeeping(pkg):
+    ctx = torch.zeros(3, 20, 4)
+    ctx[0, :5] = 1.0
+    ctx[1, :13] = 1.0
+    ctx[1, 7] = 0.0  # interior zero row does not end the sequence
+    trimmed, seqused, ln_pad = pkg.trim_context(ctx)  # item 2 all-zero -> length 1
+    assert seqused.tolist() == [5, 13, 1] and seqused.dtype == torch.int32
+    assert trimmed.shape == (3, 16, 4)  # roundup8(13)
+    torch.testing.assert_close(ln_pad, torch.log(torch.tensor([15.0, 7.0, 19.0])))
+    full = torch.ones(1, 8, 2)
+    t2, s2, l2 = pkg.trim_context(full)
+    assert t2.shape[1] == 8 and s2.tolist() == [8] and math.isinf(l2.item()) and l2.item() < 0
+
+
+def test_oracle_inputs_are_seeded_and_bf16_exact():
+    a = ref.prologue_inputs(1, 1024, 2, seed=1001)
+    b = ref.prologue_inputs(1, 1024, 2, seed=1001)
+    assert all(torch.equal(a[k], b[k]) for k in a)
+    assert torch.equal(a["qkv"], a["qkv"].to(torch.bfloat16).float())
+    assert a["cos"].shape == (1024, 64)
+
+
+def test_bench_rejects_more_than_one_gpu():
+    proc = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"],
+                          capture_output=True, text=True, timeout=300)
+    assert proc.returncode == 2
+    assert "one GPU" in proc.stderr
+
+
+def test_package_loads_once():
+    assert __graft_entry__.load_package() is __graft_entry__.load_package()
