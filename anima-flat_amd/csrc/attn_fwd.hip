@@ -447,8 +447,8 @@ extern "C" size_t aa_attn_fwd_workspace(int64_t B, int64_t Sk, int64_t H, int64_
   return (size_t)(B * H * vt_tiles(Sk)) * kTileElems * sizeof(bf16);
 }
 
-extern "C" int aa_attn_fwd(const aa_attn_fwd_args* a, void* stream) {
-  clear_error();
+// Validates args and fills the kernel parameters (no launch).
+static int prepare(const aa_attn_fwd_args* a, FwdParams& p) {
   if (!a) return fail(AA_EINVAL, "attn_fwd: null args");
   if (a->dtype != AA_DTYPE_BF16) return fail(AA_EUNSUPPORTED, "only bf16 attention is implemented");
   if (a->hd != kD) return fail(AA_EUNSUPPORTED, "head_dim must be 128");
@@ -469,7 +469,6 @@ extern "C" int aa_attn_fwd(const aa_attn_fwd_args* a, void* stream) {
   // Per-lane DMA offsets within a 64-key tile are 32-bit.
   if (std::llabs(a->k_stride[1]) >= (1 << 24) || std::llabs(a->v_stride[1]) >= (1 << 24))
     return fail(AA_EUNSUPPORTED, "attn_fwd: key/value sequence stride must be < 2^24 elements");
-
   const size_t ws_need = aa_attn_fwd_workspace(a->B, a->Sk, a->H, a->hd);
   if (ws_need > 0 && (!a->workspace || a->workspace_bytes < ws_need))
     return fail(AA_EINVAL, "attn_fwd: workspace too small");
@@ -477,7 +476,6 @@ extern "C" int aa_attn_fwd(const aa_attn_fwd_args* a, void* stream) {
     return fail(AA_EINVAL, "attn_fwd: workspace must be 16-byte aligned");
   if (vt_tiles(a->Sk) > 65535) return fail(AA_EUNSUPPORTED, "attn_fwd: Sk too large");
 
-  FwdParams p;
   p.q = (const bf16*)a->q;
   p.k = (const bf16*)a->k;
   p.v = (const bf16*)a->v;
@@ -499,12 +497,33 @@ extern "C" int aa_attn_fwd(const aa_attn_fwd_args* a, void* stream) {
   p.c = a->softmax_scale * kLog2e;
   p.ntk = (int)vt_tiles(a->Sk);
   p.vt = (const bf16*)a->workspace;
+  return AA_OK;
+}
+
+static int launch_pack(const aa_attn_fwd_args* a, const FwdParams& p, hipStream_t st) {
+  if (a->Sk == 0) return AA_OK;
+  vt_pack_kernel<<<dim3((unsigned)p.ntk, (unsigned)a->H, (unsigned)a->B), 256, 0, st>>>(
+      p.v, p.vs0, p.vs1, p.vs2, p.Sk, p.H, p.ntk, (bf16*)a->workspace);
+  return check_launch("attn_fwd vt_pack");
+}
+
+extern "C" int aa_attn_pack_v(const aa_attn_fwd_args* a, void* stream) {
+  clear_error();
+  FwdParams p;
+  if (int rc = prepare(a, p)) return rc;
+  if (a->B == 0 || a->Sq == 0) return AA_OK;
+  return launch_pack(a, p, (hipStream_t)stream);
+}
+
+extern "C" int aa_attn_fwd(const aa_attn_fwd_args* a, void* stream) {
+  clear_error();
+  FwdParams p;
+  if (int rc = prepare(a, p)) return rc;
+  if (a->B == 0 || a->Sq == 0) return AA_OK;
   hipStream_t st = (hipStream_t)stream;
-  if (a->Sk > 0) {
-    vt_pack_kernel<<<dim3((unsigned)p.ntk, (unsigned)a->H, (unsigned)a->B), 256, 0, st>>>(
-        p.v, p.vs0, p.vs1, p.vs2, p.Sk, p.H, p.ntk, (bf16*)a->workspace);
-    if (int rc = check_launch("attn_fwd vt_pack")) return rc;
+  if (!a->v_prepacked) {
+    if (int rc = launch_pack(a, p, st)) return rc;
   }
-  attn_fwd_kernel<<<dim3((unsigned)total), kWaves * 64, 0, st>>>(p);
+  attn_fwd_kernel<<<dim3((unsigned)p.total_blocks), kWaves * 64, 0, st>>>(p);
   return check_launch("attn_fwd");
 }

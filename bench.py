@@ -5,11 +5,16 @@ dense bf16 MFMA peak at 4096 tokens, 16 heads, head_dim 128 (config 2:
 B=1 self-attention, non-causal, q/k/v from the QK-RMSNorm + 3D-RoPE
 prologue on N(0,1) QKV), plus the per-denoiser-step attention time.
 
-A "step" is one forward pass of the attention kernel over the config-2 batch,
-inputs resident in HBM. Timing: W untimed steps, then K steps bracketed by
-torch.cuda.synchronize(); `value` = algorithmic FLOPs (4*B*H*Sq*Sk*d) per step
-/ mean step time. `roofline.achieved` uses the kernel's own duration from HIP
-events recorded on the launch stream around the same K launches.
+A "step" is one call of the attention forward op (anima_flat::fa_fwd_nolse)
+over the config-2 batch, inputs resident in HBM; it launches two kernels,
+vt_pack_kernel (V into transposed tiles) and attn_fwd_kernel. Timing: W untimed
+steps, then K steps bracketed by torch.cuda.synchronize(); `value` =
+algorithmic FLOPs (4*B*H*Sq*Sk*d) per step / mean wall-clock step time.
+`roofline.achieved` is the same FLOPs over attn_fwd_kernel's own mean
+duration, from HIP events on the launch stream around K launches of that
+kernel alone (V packed once beforehand); the packing kernel is timed the same
+way and reported beside it. `roofline.traffic` is read from the committed
+rocprofv3 PMC summary profiles/attn_fwd_cfg2_pmc.txt.
 
 Extra fields report the other kernels of the path: prologue and head_norm
 HBM GB/s, masked cross-attention (config 3), forward+backward (config 5),
@@ -23,6 +28,7 @@ scaled to TFLOP/s.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import math
 import os
@@ -65,6 +71,42 @@ def time_launches(fn, steps: int, warmup: int) -> tuple[float, float]:
     wall = (time.perf_counter() - t0) * 1e3 / steps
     dev = start.elapsed_time(end) / steps
     return wall, dev
+
+
+def kernel_only_timer(pkg, q, k, v):
+    """Launchers for the two kernels of one forward (V packing, attention with the
+    V already packed), called straight through the C ABI on torch's current stream."""
+    A = sys.modules[pkg.__name__ + ".attention"]
+    L = pkg._lib
+    out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    args = A._fwd_args(q, k, v, out, None, None, None)
+    nbytes = L.lib().aa_attn_fwd_workspace(q.shape[0], k.shape[1], q.shape[2], q.shape[3])
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
+    args.workspace, args.workspace_bytes = ws.data_ptr(), nbytes
+    stream = L.stream(q)
+    L.check(L.lib().aa_attn_pack_v(ctypes.byref(args), stream), "attn_pack_v")
+    packed = L.AttnFwdArgs.from_buffer_copy(args)
+    packed.v_prepacked = 1
+
+    def pack():
+        L.lib().aa_attn_pack_v(ctypes.byref(args), stream)
+
+    def attn():
+        L.lib().aa_attn_fwd(ctypes.byref(packed), stream)
+
+    return pack, attn, (out, ws)
+
+
+def pmc_traffic(name: str):
+    """HBM bytes per launch from a committed rocprofv3 PMC summary (profiles/<name>),
+    line 'traffic_bytes_per_launch: N'; None when absent."""
+    path = ROOT / "profiles" / name
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.strip().startswith("traffic_bytes_per_launch:"):
+            return int(float(line.split(":", 1)[1]))
+    return None
 
 
 def prologue_qkv(pkg, B, S, H, seed, dev):
@@ -140,6 +182,11 @@ def main() -> int:
         q, k, v = pkg.qkv_norm_rope(p["qkv"], p["q_weight"], p["k_weight"], p["cos"], p["sin"], H, eps)
         fwd = torch.ops.anima_flat.fa_fwd_nolse
         wall_ms, dev_ms = time_launches(lambda: fwd(q, k, v), args.steps, args.warmup)
+        # The dominant kernel alone: attention with V already packed; and the
+        # packing pass (vt_pack_kernel) on its own.
+        pack, attn, keep = kernel_only_timer(pkg, q, k, v)
+        _, attn_ms = time_launches(attn, args.steps, args.warmup)
+        _, pack_ms = time_launches(pack, max(10, args.steps // 2), 3)
     if args.copy_calibration:
         src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
         dst = torch.empty_like(src)
@@ -149,7 +196,7 @@ def main() -> int:
         del src, dst
     flops = attn_flops(B, H, S, S, d)
     value = flops / (wall_ms * 1e-3) / 1e12
-    achieved = flops / (dev_ms * 1e-3) / 1e12
+    achieved = flops / (attn_ms * 1e-3) / 1e12
 
     result = {
         "metric": "attn fwd TFLOP/s & % bf16 MFMA peak @4096 tok, H16 d128; per-step attn ms",
@@ -171,16 +218,19 @@ def main() -> int:
             "heads": H,
             "head_dim": d,
         },
-        "pct_of_peak": round(100.0 * achieved / PEAK_BF16_TFLOPS, 2),
+        "pct_of_peak": round(100.0 * value / PEAK_BF16_TFLOPS, 2),
+        "op_device_us": round(dev_ms * 1e3, 2),
         "roofline": {
             "bound": "mfma",
             "achieved": round(achieved, 2),
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-            "traffic": None,
+            "traffic": pmc_traffic("attn_fwd_cfg2_pmc.txt"),
             "kernel": "attn_fwd_kernel",
-            "kernel_us": round(dev_ms * 1e3, 2),
+            "kernel_us": round(attn_ms * 1e3, 2),
+            "pack_kernel": "vt_pack_kernel",
+            "pack_kernel_us": round(pack_ms * 1e3, 2),
         },
     }
 

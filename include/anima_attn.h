@@ -145,6 +145,8 @@ typedef struct aa_attn_fwd_args {
   int dtype;
   void* workspace;      /* device scratch of aa_attn_fwd_workspace() bytes */
   size_t workspace_bytes;
+  int v_prepacked;      /* nonzero: workspace already holds v packed by
+                           aa_attn_pack_v (the packing pass is skipped) */
 } aa_attn_fwd_args;
 
 /* Bytes of device workspace aa_attn_fwd needs: V repacked as transposed
@@ -162,6 +164,16 @@ size_t aa_attn_fwd_workspace(int64_t B, int64_t Sk, int64_t H, int64_t hd);
  *           src/attention.py:156-180 (cross_attention_trimmed).
  */
 int aa_attn_fwd(const aa_attn_fwd_args* args, void* stream);
+
+/*
+ * Packs args->v into args->workspace (transposed 64-key tiles) exactly as
+ * aa_attn_fwd does before its main kernel; a later aa_attn_fwd with
+ * v_prepacked = 1 and the same v, Sk, B, H reuses it (e.g. cross-attention
+ * keys/values that stay fixed across denoising steps).
+ * Replaces: no separate reference function (part of the FA4 call at
+ *           src/attention.py:63-66).
+ */
+int aa_attn_pack_v(const aa_attn_fwd_args* args, void* stream);
 
 typedef struct aa_attn_bwd_args {
   const void* dout;     /* [B, Sq, H, hd] */
