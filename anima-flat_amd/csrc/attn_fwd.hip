@@ -142,6 +142,16 @@ __device__ __forceinline__ s16x4 lds_read_tr(const bf16* p) {
 }
 
 __device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// All but the newest n tiles of this wave's DMA complete (8 instructions per
+// tile for a group-A wave: 4 K + 4 V). n is wave-uniform, 0..3.
+__device__ __forceinline__ void wait_dma_tiles_in_flight(int n) {
+  switch (n) {
+    case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+    case 1: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
+    case 2: asm volatile("s_waitcnt vmcnt(16)" ::: "memory"); break;
+    default: asm volatile("s_waitcnt vmcnt(24)" ::: "memory"); break;
+  }
+}
 
 // 16 bytes per lane from global memory straight into LDS at
 // lds_base + 16 * lane (global_load_lds_dwordx4; M0 holds the LDS base).
@@ -156,7 +166,8 @@ __device__ __forceinline__ void dma16(const void* src, const void* lds_base) {
 
 constexpr int kWaves = 8;    // two groups of 4, one wave of each group per SIMD
 constexpr int kDmaWaves = 4; // group A issues every DMA
-constexpr int kStages = 3;   // K/V ring depth
+constexpr int kStages = 4;   // K/V ring depth (4 x 32 KB)
+constexpr int kAhead = kStages - 2;  // tiles of DMA in flight beyond the next one
 constexpr int kQPerWg = kWaves * 32;
 
 // Phase-shifted ("ping-pong") schedule. Waves 0-3 (group A) and 4-7 (group B)
@@ -167,9 +178,10 @@ constexpr int kQPerWg = kWaves * 32;
 //   phase 2j+1: A runs X(j), B runs M(j)
 // with a workgroup barrier between phases. Waves w and w+4 share a SIMD, so
 // on every SIMD one wave is in an MFMA block while its partner is in a VALU
-// block and the matrix and vector pipes overlap. Tile j sits in stage j % 3;
-// its DMA is issued at phase 2j-2 and complete (wait + barrier) by the end
-// of phase 2j-1; its K is read in phases 2j, 2j+1 and its V in 2j+2, 2j+3.
+// block and the matrix and vector pipes overlap. Tile j sits in stage
+// j % kStages; its DMA is issued at phase 2(j-kAhead)+1 and complete (wait +
+// barrier) by the end of phase 2j-1; its K is read in phases 2j, 2j+1 and
+// its V in 2j+2, 2j+3.
 __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_fwd_kernel(FwdParams p) {
   constexpr int kDmaPerWave = 16 / kDmaWaves;  // 1 KB DMA blocks per group-A wave per tile, K and V each
@@ -380,27 +392,35 @@ void attn_fwd_kernel(FwdParams p) {
   // Both groups run the same instruction stream, M(m) | barrier | X(m) |
   // barrier; group B executes one extra barrier first (group A one extra at
   // the end), which shifts B by exactly one phase. Only group A issues and
-  // waits for the DMA: tile m+1 at the start of its M(m), complete before the
+  // waits for the DMA: tile m+kAhead at the start of its X(m), off the MFMA
+  // stream (the stage it overwrites held tile m+kAhead-kStages = m-2, whose V
+  // group B last read in phase 2m-1), and tile m+1 is complete before the
   // barrier that ends its X(m); the barriers order it for group B.
+  static_assert(2 * kDmaPerWave == 8, "wait_dma_tiles_in_flight counts 8 DMA per tile");
+  static_assert(kAhead >= 1 && kAhead <= 4, "lookahead");
+  auto wait_for_next = [&](int m) {  // tile m+1 complete; later issued tiles may be in flight
+    const int last_issued = min(m + kAhead, ntiles - 1);
+    wait_dma_tiles_in_flight(max(last_issued - (m + 1), 0));
+  };
   if (group_a && ntiles > 0) {
-    issue_tile(0);
-    wait_dma();
+    for (int t = 0; t < kAhead && t < ntiles; ++t) issue_tile(t);
+    wait_for_next(-1);
   }
   __syncthreads();
   if (!group_a) __syncthreads();
   if (ntiles > 0) {
-    if (group_a && 1 < ntiles) issue_tile(1);
     mblock(0, 0, std::false_type{}, std::true_type{});
     __syncthreads();
+    if (group_a && kAhead < ntiles) issue_tile(kAhead);
     softmax(0);
-    if (group_a) wait_dma();
+    if (group_a) wait_for_next(0);
     __syncthreads();
     for (int m = 1; m < ntiles; ++m) {
-      if (group_a && m + 1 < ntiles) issue_tile(m + 1);
       mblock(m - 1, m, std::true_type{}, std::true_type{});
       __syncthreads();
+      if (group_a && m + kAhead < ntiles) issue_tile(m + kAhead);
       softmax(m);
-      if (group_a) wait_dma();
+      if (group_a) wait_for_next(m);
       __syncthreads();
     }
     mblock(ntiles - 1, ntiles - 1, std::true_type{}, std::false_type{});
