@@ -1,81 +1,39 @@
 // Flash-attention backward, non-causal, head_dim 128, bf16 in / fp32 accumulate,
-// for gfx950 (v_mfma_f32_32x32x16_bf16). Deterministic: three kernels, no
-// atomics, every reduction in a fixed order.
+// for gfx950 (v_mfma_f32_32x32x16_bf16). Deterministic: no atomics, every
+// reduction in a fixed order.
 //
 //   z = scale * q k^T, P = softmax(z) (recomputed from the forward LSE),
 //   dV = P^T dO, dP = dO V^T, dZ = P o (dP - D) with D = rowsum(dO o O),
 //   dK = scale * dZ^T Q, dQ = scale * dZ K.
 //
-// 1. rowdot_kernel: D[b,h,q] = sum_d dO*O in fp32.
-// 2. dkdv_kernel: one workgroup per 128 keys (4 waves x 32 keys); loops over
-//    64-query tiles staged in LDS (row-major and transposed copies of Q and
-//    dO). Per wave and tile, with keys as accumulator columns (lane%32):
-//      S  = Q K^T      (A = Q rows from LDS,  B = K^T from registers)
-//      dP = dO V^T     (A = dO rows from LDS, B = V^T from registers)
-//      dV^T += dO^T P  (A = dO^T from LDS,    B = P from the S accumulators)
-//      dK^T += Q^T dZ  (A = Q^T from LDS,     B = dZ from the accumulators)
-// 3. dq_kernel: one workgroup per 128 queries (4 waves x 32 queries); loops
-//    over 64-key tiles (K row-major and transposed, V row-major). With
-//    queries as columns:
+// Three kernels:
+// 1. prep_kernel, one workgroup per (64-row tile, head, batch): writes the
+//    transposed tiles Q^T, dO^T (columns = queries) and K^T (columns = keys)
+//    in the tile_io.h format, and per 64-query tile a 1 KB record of
+//    lse * log2(e) and D.
+// 2. dkdv_kernel: 4 waves x 32 keys per workgroup; streams 64-query tiles
+//    (Q rows, dO rows, Q^T, dO^T, stats: 65 KB, two stages) into LDS by DMA.
+//    Keys are the accumulator columns (lane % 32), K and V sit in registers:
+//      S  = Q K^T        A = Q rows (LDS),  B = K^T (registers)
+//      dP = dO V^T       A = dO rows (LDS), B = V^T (registers)
+//      dV^T += dO^T P    A = dO^T (LDS),    B = P from the S accumulators
+//      dK^T += Q^T dZ    A = Q^T (LDS),     B = dZ from the accumulators
+// 3. dq_kernel: 4 waves x 32 queries per workgroup; streams 64-key tiles
+//    (K rows, V rows, K^T: 48 KB, two stages). Queries are the columns:
 //      S^T = K Q^T, dP^T = V dO^T, dQ^T += K^T dZ^T.
-// Transposed LDS copies use the same permuted row order inside each group of
-// 16 rows as the forward kernel's V^T (position 8h+4g+i <-> row 8g+4h+i), so
-// the accumulator registers feed the next MFMA as B operands unchanged.
-#include "aa_common.h"
+// The transposed tiles list their columns in the accumulator row order
+// (tt_col), so the bf16-rounded accumulators are the B operands as they are.
+#include "tile_io.h"
 
 namespace aa {
 
 namespace bwd {
 
 constexpr int kD = 128;
-constexpr int kT = 64;               // rows (queries or keys) per streamed tile
-constexpr int kRStride = kD + 8;     // row-major tile stride (elements)
-constexpr int kTStride = kT + 8;     // transposed tile stride (elements)
-constexpr int kRTile = kT * kRStride;
-constexpr int kTTile = kD * kTStride;
+constexpr int kT = kTileRows;  // rows (queries or keys) per streamed tile
+constexpr int kStat = 256;     // floats per 64-query stats record: lse2[64], D[64], zero pad
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
-
-// Thread unit of a 64 x 128 tile: rows 4*g4 .. 4*g4+3, d columns 8*dc .. 8*dc+7
-// (g4 = tid & 15, dc = tid >> 4; 256 threads cover the tile).
-struct Unit {
-  u32x4 r[4];
-};
-
-__device__ __forceinline__ void load_unit(Unit& u, const bf16* base, int64_t rstride, int row0,
-                                          int nvalid, int g4, int dc) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = row0 + 4 * g4 + i;
-    u32x4 w = {0u, 0u, 0u, 0u};
-    if (row < nvalid) w = ld16(base + (int64_t)row * rstride + 8 * dc);
-    u.r[i] = w;
-  }
-}
-
-__device__ __forceinline__ void store_rows(const Unit& u, bf16* tile, int g4, int dc) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) st16(tile + (4 * g4 + i) * kRStride + 8 * dc, u.r[i]);
-}
-
-__device__ __forceinline__ int perm_pos(int g4) {
-  return 16 * (g4 >> 2) + 8 * (g4 & 1) + 4 * ((g4 >> 1) & 1);
-}
-
-__device__ __forceinline__ void store_transposed(const Unit& u, bf16* tile, int g4, int dc) {
-  const int pos = perm_pos(g4);
-#pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    const uint32_t a0 = u.r[0][m], a1 = u.r[1][m], a2 = u.r[2][m], a3 = u.r[3][m];
-    u32x2 lo = {(a0 & 0xffffu) | (a1 << 16), (a2 & 0xffffu) | (a3 << 16)};
-    u32x2 hi = {(a0 >> 16) | (a1 & 0xffff0000u), (a2 >> 16) | (a3 & 0xffff0000u)};
-    *reinterpret_cast<u32x2*>(tile + (8 * dc + 2 * m) * kTStride + pos) = lo;
-    *reinterpret_cast<u32x2*>(tile + (8 * dc + 2 * m + 1) * kTStride + pos) = hi;
-  }
-}
-
-// Row index held by accumulator register r of a 32x32 MFMA tile, lane half hh.
-__device__ __forceinline__ int acc_row(int r, int hh) { return 8 * (r >> 2) + 4 * hh + (r & 3); }
 
 struct Params {
   const bf16* dout;
@@ -84,54 +42,84 @@ struct Params {
   const bf16* v;
   const bf16* o;
   const float* lse;
-  float* delta;  // [B, H, Sq]
   bf16* dq;
   bf16* dk;
   bf16* dv;
   int64_t s_do[3], s_q[3], s_k[3], s_v[3], s_o[3], s_dq[3], s_dk[3], s_dv[3];
-  int H, Sq, Sk;
+  bf16* qT;      // [B][H][ntq][8192] transposed Q tiles
+  bf16* doT;     // [B][H][ntq][8192] transposed dO tiles
+  bf16* kT;      // [B][H][ntk][8192] transposed K tiles
+  float* stats;  // [B][H][ntq][kStat]
+  int H, Sq, Sk, ntq, ntk;
   float c;      // scale * log2(e)
   float scale;  // softmax scale
 };
 
-// D = rowsum(dO * O): 16 lanes per (b, q, h) row of 128.
-__global__ __launch_bounds__(256) void rowdot_kernel(Params p, int64_t nrow) {
-  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t row = gid >> 4;
-  if (row >= nrow) return;
-  const int lane = (int)(gid & 15);
-  // row = ((b * Sq) + q) * H + h
-  const int h = (int)(row % p.H);
-  const int64_t bq = row / p.H;
-  const int q = (int)(bq % p.Sq);
-  const int b = (int)(bq / p.Sq);
-  float x[8], y[8];
-  unpack8(ld16(p.dout + b * p.s_do[0] + (int64_t)q * p.s_do[1] + h * p.s_do[2] + 8 * lane), x);
-  unpack8(ld16(p.o + b * p.s_o[0] + (int64_t)q * p.s_o[1] + h * p.s_o[2] + 8 * lane), y);
-  float s = 0.f;
+// ---------------------------------------------------------------- prep --
+
+__global__ __launch_bounds__(256) void prep_kernel(Params p) {
+  __shared__ __attribute__((aligned(16))) bf16 stage[kT * kPackRow];
+  const int t = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int64_t bh = (int64_t)b * p.H + h;
+  const int tid = threadIdx.x;
+  if (t < p.ntq) {
+    const int q0 = t * kT;
+    pack_transposed_tile(p.q + b * p.s_q[0] + h * p.s_q[2], p.s_q[1], q0, p.Sq,
+                         p.qT + (bh * p.ntq + t) * kTileElems, stage);
+    pack_transposed_tile(p.dout + b * p.s_do[0] + h * p.s_do[2], p.s_do[1], q0, p.Sq,
+                         p.doT + (bh * p.ntq + t) * kTileElems, stage);
+    // D = rowsum(dO * O): 4 lanes per row, 32 values each. Rows past Sq get
+    // lse2 = +inf (P = 0) and D = 0.
+    const int row = tid >> 2, part = tid & 3;
+    const int q = q0 + row;
+    float d = 0.f;
+    if (q < p.Sq) {
+      const bf16* dop = p.dout + b * p.s_do[0] + (int64_t)q * p.s_do[1] + h * p.s_do[2] + 32 * part;
+      const bf16* op = p.o + b * p.s_o[0] + (int64_t)q * p.s_o[1] + h * p.s_o[2] + 32 * part;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) s += x[i] * y[i];
-  s = group_sum<16>(s);
-  if (lane == 0) p.delta[((int64_t)b * p.H + h) * p.Sq + q] = s;
+      for (int j = 0; j < 4; ++j) {
+        float x[8], y[8];
+        unpack8(ld16(dop + 8 * j), x);
+        unpack8(ld16(op + 8 * j), y);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) d = fmaf(x[i], y[i], d);
+      }
+    }
+    d = group_sum<4>(d);
+    float* st = p.stats + (bh * p.ntq + t) * kStat;
+    if (part == 0) {
+      st[row] = q < p.Sq ? p.lse[bh * p.Sq + q] * kLog2e : INFINITY;
+      st[kT + row] = d;
+    }
+    if (tid < kStat - 2 * kT) st[2 * kT + tid] = 0.f;
+  }
+  if (t < p.ntk) {
+    pack_transposed_tile(p.k + b * p.s_k[0] + h * p.s_k[2], p.s_k[1], t * kT, p.Sk,
+                         p.kT + (bh * p.ntk + t) * kTileElems, stage);
+  }
 }
 
-// ------------------------------------------------------------------ dK, dV --
+// ------------------------------------------------------------ dK, dV --
 
 constexpr int kKeysPerWg = 128;  // 4 waves x 32 keys
+constexpr int kQueue = 8;        // LDS operands in flight ahead of the MFMA that uses them
 
-__global__ __launch_bounds__(256) void dkdv_kernel(Params p, int nkblk) {
-  // Two stages x {Q rows, Q^T, dO rows, dO^T} + per-query lse2 and D.
-  constexpr int kStage = 2 * kRTile + 2 * kTTile;
-  __shared__ __attribute__((aligned(16))) bf16 smem[2 * kStage];
-  __shared__ __attribute__((aligned(16))) float rowstat[2][2][kT];  // [stage][lse2 | D][query]
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void dkdv_kernel(Params p, int nkblk, int total_blocks) {
+  // Per stage: Q rows, dO rows (row tiles), Q^T, dO^T (transposed tiles).
+  __shared__ __attribute__((aligned(1024))) bf16 tiles[2][4][kTileElems];
+  __shared__ __attribute__((aligned(1024))) float stat[2][kStat];
 
-  const int kblk = blockIdx.x % nkblk;
-  const int bh = blockIdx.x / nkblk;
+  const int logical = xcd_remap(blockIdx.x, total_blocks);
+  const int kblk = logical % nkblk;
+  const int bh = logical / nkblk;
   const int b = bh / p.H, h = bh - (bh / p.H) * p.H;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
   const int li = lane & 31, hh = lane >> 5;
-  const int g4 = tid & 15, dc = tid >> 4;
 
+  // K^T / V^T operands: lane holds K[key][16 kk + 8 hh + 0..7].
   const int key = kblk * kKeysPerWg + wave * 32 + li;
   const bool key_ok = key < p.Sk;
   bf16x8 kreg[8], vreg[8];
@@ -152,29 +140,40 @@ __global__ __launch_bounds__(256) void dkdv_kernel(Params p, int nkblk) {
 
   const bf16* qbase = p.q + b * p.s_q[0] + h * p.s_q[2];
   const bf16* dobase = p.dout + b * p.s_do[0] + h * p.s_do[2];
-  const float* lse = p.lse + ((int64_t)b * p.H + h) * p.Sq;
-  const float* delta = p.delta + ((int64_t)b * p.H + h) * p.Sq;
-  const int ntiles = (p.Sq + kT - 1) / kT;
+  const bf16* qTb = p.qT + (int64_t)bh * p.ntq * kTileElems;
+  const bf16* doTb = p.doT + (int64_t)bh * p.ntq * kTileElems;
+  const float* statb = p.stats + (int64_t)bh * p.ntq * kStat;
+  const int ntiles = p.ntq;
 
-  Unit uq, udo;
-  float stat = 0.f;
-  auto load_tile = [&](int t) {
-    load_unit(uq, qbase, p.s_q[1], t * kT, p.Sq, g4, dc);
-    load_unit(udo, dobase, p.s_do[1], t * kT, p.Sq, g4, dc);
-    if (tid < 2 * kT) {
-      const int qq = t * kT + (tid & (kT - 1));
-      if (tid < kT) stat = qq < p.Sq ? lse[qq] * kLog2e : INFINITY;
-      else stat = qq < p.Sq ? delta[qq] : 0.f;
+  // Each wave copies 4 of the 16 blocks of each of the 4 tiles (its DMA
+  // j = 0..15: tile j / 4, block 4 wave + j % 4); wave 0 also the stats.
+  auto issue_block = [&](int t, int st, int j) {
+    const int blk = 4 * wave + (j & 3);
+    const int q0 = t * kT;
+    switch (j >> 2) {
+      case 0:
+        dma_row_block(qbase + (int64_t)q0 * p.s_q[1], p.s_q[1], min(kT, p.Sq - q0), tiles[st][0],
+                      blk, lane);
+        break;
+      case 1:
+        dma_row_block(dobase + (int64_t)q0 * p.s_do[1], p.s_do[1], min(kT, p.Sq - q0),
+                      tiles[st][1], blk, lane);
+        break;
+      case 2:
+        dma16(qTb + (int64_t)t * kTileElems + blk * 512 + lane * 8, tiles[st][2] + blk * 512);
+        break;
+      default:
+        dma16(doTb + (int64_t)t * kTileElems + blk * 512 + lane * 8, tiles[st][3] + blk * 512);
+        break;
     }
   };
-  auto store_tile = [&](int st) {
-    bf16* base = smem + st * kStage;
-    store_rows(uq, base, g4, dc);
-    store_transposed(uq, base + kRTile, g4, dc);
-    store_rows(udo, base + kRTile + kTTile, g4, dc);
-    store_transposed(udo, base + 2 * kRTile + kTTile, g4, dc);
-    if (tid < 2 * kT) rowstat[st][tid >> 6][tid & (kT - 1)] = stat;
+  auto issue_stats = [&](int t, int st) {
+    if (wave == 0) dma16(statb + (int64_t)t * kStat + 4 * lane, stat[st]);
   };
+
+  const int r_rd = row_rd(lane);
+  const int t_rd = tt_rd(lane);
+  const float c = p.c;
 
   f32x16 dk[4], dv[4];
 #pragma unroll
@@ -186,71 +185,99 @@ __global__ __launch_bounds__(256) void dkdv_kernel(Params p, int nkblk) {
     }
 
   if (ntiles > 0) {
-    load_tile(0);
-    store_tile(0);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) issue_block(0, 0, j);
+    issue_stats(0, 0);
+    wait_dma();
   }
   __syncthreads();
 
   for (int t = 0; t < ntiles; ++t) {
     const int st = t & 1;
-    const bf16* qrows = smem + st * kStage;
-    const bf16* qT = qrows + kRTile;
-    const bf16* dorows = qT + kTTile;
-    const bf16* doT = dorows + kRTile;
-    if (t + 1 < ntiles) load_tile(t + 1);
+    // Tile t+1 goes to the other stage, which held tile t-1 (all its reads
+    // ended before the last barrier). Its 16 DMA instructions are spread over
+    // the MFMA stream, one every 4 ops: issued back to back they stall the
+    // wave while the CU's address path drains them.
+    const bool more = t + 1 < ntiles;
+    if (more) issue_stats(t + 1, st ^ 1);
+    const bf16* qr = tiles[st][0];
+    const bf16* dor = tiles[st][1];
+    const bf16* qt = tiles[st][2];
+    const bf16* dot = tiles[st][3];
 
-    // S = Q K^T and dP = dO V^T for two 32-query halves.
+    // One unrolled stream of 64 MFMAs, A operands read from LDS kQueue ops
+    // ahead (sched_barrier fences keep the order):
+    //   ops 0-31 : kk = i / 4, half hq = (i / 2) % 2;
+    //              even: S[hq] += Q rows x K^T, odd: dP[hq] += dO rows x V^T
+    //   ops 32-63: c4 = j / 8, dt = (j / 2) % 4 (j = i - 32);
+    //              even: dV^T[dt] += dO^T x P, odd: dK^T[dt] += Q^T x dZ
+    // P and dZ are formed between op 31 and op 32, while the first operands
+    // of the second half are already in flight.
     f32x16 s[2], dp[2];
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
+    for (int hq = 0; hq < 2; ++hq)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        s[qt][r] = 0.f;
-        dp[qt][r] = 0.f;
+        s[hq][r] = 0.f;
+        dp[hq][r] = 0.f;
       }
-      const bf16* qa = qrows + (32 * qt + li) * kRStride + 8 * hh;
-      const bf16* da = dorows + (32 * qt + li) * kRStride + 8 * hh;
-#pragma unroll
-      for (int kk = 0; kk < 8; ++kk) {
-        s[qt] = mfma32(*reinterpret_cast<const bf16x8*>(qa + 16 * kk), kreg[kk], s[qt]);
-        dp[qt] = mfma32(*reinterpret_cast<const bf16x8*>(da + 16 * kk), vreg[kk], dp[qt]);
-      }
-    }
-
-    // P = exp2(S c - lse2[q]); dZ = P (dP - D[q]). Rows are queries.
     bf16x8 pb[4], zb[4];
+    auto load_op = [&](int i) -> bf16x8 {
+      if (i < 32) {
+        const int kk = i >> 2, hq = (i >> 1) & 1;
+        return *reinterpret_cast<const bf16x8*>(((i & 1) ? dor : qr) + r_rd + 4096 * hq + 256 * kk);
+      }
+      const int j = i - 32, c4 = j >> 3, dt = (j >> 1) & 3;
+      return *reinterpret_cast<const bf16x8*>(((j & 1) ? qt : dot) + t_rd + 2048 * dt + 256 * c4);
+    };
+    auto run_op = [&](int i, bf16x8 a) {
+      if (i < 32) {
+        const int kk = i >> 2, hq = (i >> 1) & 1;
+        if (i & 1) dp[hq] = mfma32(a, vreg[kk], dp[hq]);
+        else s[hq] = mfma32(a, kreg[kk], s[hq]);
+      } else {
+        const int j = i - 32, c4 = j >> 3, dt = (j >> 1) & 3;
+        if (j & 1) dk[dt] = mfma32(a, zb[c4], dk[dt]);
+        else dv[dt] = mfma32(a, pb[c4], dv[dt]);
+      }
+    };
+    // P = exp2(S c - lse2[q]); dZ = P (dP - D[q]). Register r of half hq is
+    // query 32 hq + 8 (r >> 2) + 4 hh + (r & 3).
+    auto form_p_dz = [&]() {
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
+      for (int hq = 0; hq < 2; ++hq) {
 #pragma unroll
-      for (int rq = 0; rq < 4; ++rq) {
-        const int q0 = 32 * qt + 8 * rq + 4 * hh;
-        const f32x4 l2 = *reinterpret_cast<const f32x4*>(&rowstat[st][0][q0]);
-        const f32x4 dd = *reinterpret_cast<const f32x4*>(&rowstat[st][1][q0]);
+        for (int rq = 0; rq < 4; ++rq) {
+          const int q0 = 32 * hq + 8 * rq + 4 * hh;
+          const f32x4 l2 = *reinterpret_cast<const f32x4*>(&stat[st][q0]);
+          const f32x4 dd = *reinterpret_cast<const f32x4*>(&stat[st][kT + q0]);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int r = 4 * rq + i;
-          const float pv = fast_exp2(s[qt][r] * p.c - l2[i]);
-          const float zv = pv * (dp[qt][r] - dd[i]);
-          const int c4 = 2 * qt + (r >> 3);
-          pb[c4][r & 7] = (bf16)pv;
-          zb[c4][r & 7] = (bf16)zv;
+          for (int i = 0; i < 4; ++i) {
+            const int r = 4 * rq + i;
+            const float pv = fast_exp2(fmaf(s[hq][r], c, -l2[i]));
+            const float zv = pv * (dp[hq][r] - dd[i]);
+            const int c4 = 2 * hq + (r >> 3);
+            pb[c4][r & 7] = (bf16)pv;
+            zb[c4][r & 7] = (bf16)zv;
+          }
         }
       }
-    }
-
-    // dV^T += dO^T P, dK^T += Q^T dZ.
+    };
+    bf16x8 queue[kQueue];
+    auto step = [&](int i) {  // run op i - kQueue, then load op i into its slot
+      const int u = i - kQueue;
+      if (u >= 0) run_op(u, queue[u % kQueue]);
+      if (i < 64) queue[i % kQueue] = load_op(i);
+      if ((i & 3) == 1 && (i >> 2) < 16 && more) issue_block(t + 1, st ^ 1, i >> 2);
+      __builtin_amdgcn_sched_barrier(0);
+    };
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
-      const bf16* doa = doT + (32 * dt + li) * kTStride + 8 * hh;
-      const bf16* qa = qT + (32 * dt + li) * kTStride + 8 * hh;
+    for (int i = 0; i < 32 + kQueue; ++i) step(i);
+    form_p_dz();
 #pragma unroll
-      for (int c4 = 0; c4 < 4; ++c4) {
-        dv[dt] = mfma32(*reinterpret_cast<const bf16x8*>(doa + 16 * c4), pb[c4], dv[dt]);
-        dk[dt] = mfma32(*reinterpret_cast<const bf16x8*>(qa + 16 * c4), zb[c4], dk[dt]);
-      }
-    }
+    for (int i = 32 + kQueue; i < 64 + kQueue; ++i) step(i);
 
-    if (t + 1 < ntiles) store_tile(st ^ 1);
+    wait_dma();
     __syncthreads();
   }
 
@@ -262,10 +289,10 @@ __global__ __launch_bounds__(256) void dkdv_kernel(Params p, int nkblk) {
 #pragma unroll
       for (int rq = 0; rq < 4; ++rq) {
         const f32x16& a = dk[dt];
-        const f32x16& c = dv[dt];
+        const f32x16& e = dv[dt];
         u32x2 wk = {pack_bf16(a[4 * rq] * p.scale, a[4 * rq + 1] * p.scale),
                     pack_bf16(a[4 * rq + 2] * p.scale, a[4 * rq + 3] * p.scale)};
-        u32x2 wv = {pack_bf16(c[4 * rq], c[4 * rq + 1]), pack_bf16(c[4 * rq + 2], c[4 * rq + 3])};
+        u32x2 wv = {pack_bf16(e[4 * rq], e[4 * rq + 1]), pack_bf16(e[4 * rq + 2], e[4 * rq + 3])};
         *reinterpret_cast<u32x2*>(dkp + 32 * dt + 8 * rq) = wk;
         *reinterpret_cast<u32x2*>(dvp + 32 * dt + 8 * rq) = wv;
       }
@@ -273,21 +300,25 @@ __global__ __launch_bounds__(256) void dkdv_kernel(Params p, int nkblk) {
   }
 }
 
-// ---------------------------------------------------------------------- dQ --
+// ------------------------------------------------------------------ dQ --
 
 constexpr int kQueriesPerWg = 128;  // 4 waves x 32 queries
 
-__global__ __launch_bounds__(256) void dq_kernel(Params p, int nqblk) {
-  constexpr int kStage = 2 * kRTile + kTTile;  // K rows, K^T, V rows
-  __shared__ __attribute__((aligned(16))) bf16 smem[2 * kStage];
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void dq_kernel(Params p, int nqblk, int total_blocks) {
+  // Per stage: K rows, V rows (row tiles), K^T (transposed tile).
+  __shared__ __attribute__((aligned(1024))) bf16 tiles[2][3][kTileElems];
 
-  const int qblk = blockIdx.x % nqblk;
-  const int bh = blockIdx.x / nqblk;
+  const int logical = xcd_remap(blockIdx.x, total_blocks);
+  const int qblk = logical % nqblk;
+  const int bh = logical / nqblk;
   const int b = bh / p.H, h = bh - (bh / p.H) * p.H;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
   const int li = lane & 31, hh = lane >> 5;
-  const int g4 = tid & 15, dc = tid >> 4;
 
+  // Q^T / dO^T operands: lane holds Q[query][16 kk + 8 hh + 0..7].
   const int qrow = qblk * kQueriesPerWg + wave * 32 + li;
   const bool q_ok = qrow < p.Sq;
   bf16x8 qreg[8], doreg[8];
@@ -296,34 +327,49 @@ __global__ __launch_bounds__(256) void dq_kernel(Params p, int nqblk) {
     const bf16* dp = p.dout + b * p.s_do[0] + h * p.s_do[2] + (int64_t)qrow * p.s_do[1] + 8 * hh;
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk) {
-      u32x4 a = {0u, 0u, 0u, 0u}, c = {0u, 0u, 0u, 0u};
+      u32x4 a = {0u, 0u, 0u, 0u}, e = {0u, 0u, 0u, 0u};
       if (q_ok) {
         a = ld16(qp + 16 * kk);
-        c = ld16(dp + 16 * kk);
+        e = ld16(dp + 16 * kk);
       }
       qreg[kk] = as_bf16x8(a);
-      doreg[kk] = as_bf16x8(c);
+      doreg[kk] = as_bf16x8(e);
     }
   }
-  const int64_t srow = ((int64_t)b * p.H + h) * p.Sq + qrow;
-  const float lse2 = q_ok ? p.lse[srow] * kLog2e : INFINITY;
-  const float dlt = q_ok ? p.delta[srow] : 0.f;
+  float lse2 = INFINITY, dlt = 0.f;
+  if (q_ok) {
+    const float* st = p.stats + ((int64_t)bh * p.ntq + qrow / kT) * kStat + (qrow % kT);
+    lse2 = st[0];
+    dlt = st[kT];
+  }
 
   const bf16* kbase = p.k + b * p.s_k[0] + h * p.s_k[2];
   const bf16* vbase = p.v + b * p.s_v[0] + h * p.s_v[2];
-  const int ntiles = (p.Sk + kT - 1) / kT;
+  const bf16* kTb = p.kT + (int64_t)bh * p.ntk * kTileElems;
+  const int ntiles = p.ntk;
 
-  Unit uk, uv;
-  auto load_tile = [&](int t) {
-    load_unit(uk, kbase, p.s_k[1], t * kT, p.Sk, g4, dc);
-    load_unit(uv, vbase, p.s_v[1], t * kT, p.Sk, g4, dc);
+  // Wave DMA j = 0..11: tile j / 4 (K rows, V rows, K^T), block 4 wave + j % 4.
+  auto issue_block = [&](int t, int st, int j) {
+    const int blk = 4 * wave + (j & 3);
+    const int k0 = t * kT;
+    switch (j >> 2) {
+      case 0:
+        dma_row_block(kbase + (int64_t)k0 * p.s_k[1], p.s_k[1], min(kT, p.Sk - k0), tiles[st][0],
+                      blk, lane);
+        break;
+      case 1:
+        dma_row_block(vbase + (int64_t)k0 * p.s_v[1], p.s_v[1], min(kT, p.Sk - k0), tiles[st][1],
+                      blk, lane);
+        break;
+      default:
+        dma16(kTb + (int64_t)t * kTileElems + blk * 512 + lane * 8, tiles[st][2] + blk * 512);
+        break;
+    }
   };
-  auto store_tile = [&](int st) {
-    bf16* base = smem + st * kStage;
-    store_rows(uk, base, g4, dc);
-    store_transposed(uk, base + kRTile, g4, dc);
-    store_rows(uv, base + kRTile + kTTile, g4, dc);
-  };
+
+  const int r_rd = row_rd(lane);
+  const int t_rd = tt_rd(lane);
+  const float c = p.c;
 
   f32x16 dq[4];
 #pragma unroll
@@ -332,59 +378,81 @@ __global__ __launch_bounds__(256) void dq_kernel(Params p, int nqblk) {
     for (int r = 0; r < 16; ++r) dq[i][r] = 0.f;
 
   if (ntiles > 0) {
-    load_tile(0);
-    store_tile(0);
+#pragma unroll
+    for (int j = 0; j < 12; ++j) issue_block(0, 0, j);
+    wait_dma();
   }
   __syncthreads();
 
   for (int t = 0; t < ntiles; ++t) {
     const int st = t & 1;
-    const bf16* krows = smem + st * kStage;
-    const bf16* kT_ = krows + kRTile;
-    const bf16* vrows = kT_ + kTTile;
-    if (t + 1 < ntiles) load_tile(t + 1);
+    // Tile t+1 into the other stage, its 12 DMA spread over the MFMA stream.
+    const bool more = t + 1 < ntiles;
+    const bf16* kr = tiles[st][0];
+    const bf16* vr = tiles[st][1];
+    const bf16* kt = tiles[st][2];
 
+    // One unrolled stream of 48 MFMAs with a kQueue-deep operand queue:
+    //   ops 0-31 : kk = i / 4, half hk = (i / 2) % 2;
+    //              even: S^T[hk] += K rows x Q^T, odd: dP^T[hk] += V rows x dO^T
+    //   ops 32-47: c4 = j / 4, dt = j % 4 (j = i - 32): dQ^T[dt] += K^T x dZ^T
     f32x16 s[2], dp[2];
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
+    for (int hk = 0; hk < 2; ++hk)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        s[kt][r] = 0.f;
-        dp[kt][r] = 0.f;
+        s[hk][r] = 0.f;
+        dp[hk][r] = 0.f;
       }
-      const bf16* ka = krows + (32 * kt + li) * kRStride + 8 * hh;
-      const bf16* va = vrows + (32 * kt + li) * kRStride + 8 * hh;
-#pragma unroll
-      for (int kk = 0; kk < 8; ++kk) {
-        s[kt] = mfma32(*reinterpret_cast<const bf16x8*>(ka + 16 * kk), qreg[kk], s[kt]);
-        dp[kt] = mfma32(*reinterpret_cast<const bf16x8*>(va + 16 * kk), doreg[kk], dp[kt]);
+    bf16x8 zb[4];
+    auto load_op = [&](int i) -> bf16x8 {
+      if (i < 32) {
+        const int kk = i >> 2, hk = (i >> 1) & 1;
+        return *reinterpret_cast<const bf16x8*>(((i & 1) ? vr : kr) + r_rd + 4096 * hk + 256 * kk);
       }
-    }
-
+      const int j = i - 32, c4 = j >> 2, dt = j & 3;
+      return *reinterpret_cast<const bf16x8*>(kt + t_rd + 2048 * dt + 256 * c4);
+    };
+    auto run_op = [&](int i, bf16x8 a) {
+      if (i < 32) {
+        const int kk = i >> 2, hk = (i >> 1) & 1;
+        if (i & 1) dp[hk] = mfma32(a, doreg[kk], dp[hk]);
+        else s[hk] = mfma32(a, qreg[kk], s[hk]);
+      } else {
+        const int j = i - 32, c4 = j >> 2, dt = j & 3;
+        dq[dt] = mfma32(a, zb[c4], dq[dt]);
+      }
+    };
+    // Register r of half hk is key kb + 32 hk + 8 (r >> 2) + 4 hh + (r & 3);
+    // keys past Sk (last tile) get P = 0.
     const int kb = t * kT;
     const bool partial = kb + kT > p.Sk;
-    bf16x8 zb[4];
+    auto form_dz = [&]() {
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
+      for (int hk = 0; hk < 2; ++hk) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float pv = fast_exp2(s[kt][r] * p.c - lse2);
-        if (partial && kb + 32 * kt + acc_row(r, hh) >= p.Sk) pv = 0.f;
-        const float zv = pv * (dp[kt][r] - dlt);
-        zb[2 * kt + (r >> 3)][r & 7] = (bf16)zv;
+        for (int r = 0; r < 16; ++r) {
+          float pv = fast_exp2(fmaf(s[hk][r], c, -lse2));
+          if (partial && kb + 32 * hk + 8 * (r >> 2) + 4 * hh + (r & 3) >= p.Sk) pv = 0.f;
+          zb[2 * hk + (r >> 3)][r & 7] = (bf16)(pv * (dp[hk][r] - dlt));
+        }
       }
-    }
-
+    };
+    bf16x8 queue[kQueue];
+    auto step = [&](int i) {  // run op i - kQueue, then load op i into its slot
+      const int u = i - kQueue;
+      if (u >= 0) run_op(u, queue[u % kQueue]);
+      if (i < 48) queue[i % kQueue] = load_op(i);
+      if ((i & 3) == 1 && (i >> 2) < 12 && more) issue_block(t + 1, st ^ 1, i >> 2);
+      __builtin_amdgcn_sched_barrier(0);
+    };
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
-      const bf16* ka = kT_ + (32 * dt + li) * kTStride + 8 * hh;
+    for (int i = 0; i < 32 + kQueue; ++i) step(i);
+    form_dz();
 #pragma unroll
-      for (int c4 = 0; c4 < 4; ++c4) {
-        dq[dt] = mfma32(*reinterpret_cast<const bf16x8*>(ka + 16 * c4), zb[c4], dq[dt]);
-      }
-    }
+    for (int i = 32 + kQueue; i < 48 + kQueue; ++i) step(i);
 
-    if (t + 1 < ntiles) store_tile(st ^ 1);
+    wait_dma();
     __syncthreads();
   }
 
@@ -404,7 +472,24 @@ __global__ __launch_bounds__(256) void dq_kernel(Params p, int nqblk) {
 }
 
 static bool stride_ok(const int64_t* s) {
-  return (s[0] % 8) == 0 && (s[1] % 8) == 0 && (s[2] % 8) == 0;
+  return (s[0] % 8) == 0 && (s[1] % 8) == 0 && (s[2] % 8) == 0 && s[0] < (1ll << 40) &&
+         s[1] < (1ll << 40) && s[2] < (1ll << 40);
+}
+
+struct WsLayout {
+  size_t qT, doT, kT, stats, total;
+};
+
+static WsLayout ws_layout(int64_t B, int64_t Sq, int64_t Sk, int64_t H) {
+  const int64_t ntq = (Sq + kT - 1) / kT, ntk = (Sk + kT - 1) / kT;
+  const size_t tile = (size_t)kTileElems * sizeof(bf16);
+  WsLayout w;
+  w.qT = 0;
+  w.doT = w.qT + (size_t)(B * H * ntq) * tile;
+  w.kT = w.doT + (size_t)(B * H * ntq) * tile;
+  w.stats = w.kT + (size_t)(B * H * ntk) * tile;
+  w.total = w.stats + (size_t)(B * H * ntq) * kStat * sizeof(float);
+  return w;
 }
 
 }  // namespace bwd
@@ -413,10 +498,9 @@ static bool stride_ok(const int64_t* s) {
 using namespace aa;
 
 extern "C" size_t aa_attn_bwd_workspace(int64_t B, int64_t Sq, int64_t Sk, int64_t H, int64_t hd) {
-  (void)Sk;
   (void)hd;
-  if (B <= 0 || Sq <= 0 || H <= 0) return 0;
-  return (size_t)(B * H * Sq) * sizeof(float);
+  if (B <= 0 || Sq <= 0 || H <= 0 || Sk < 0) return 0;
+  return bwd::ws_layout(B, Sq, Sk, H).total;
 }
 
 extern "C" int aa_attn_bwd(const aa_attn_bwd_args* a, void* workspace, size_t workspace_bytes,
@@ -440,9 +524,13 @@ extern "C" int aa_attn_bwd(const aa_attn_bwd_args* a, void* workspace, size_t wo
                               a->out_stride,  a->dq_stride, a->dk_stride, a->dv_stride};
   for (const int64_t* s : strides)
     if (!bwd::stride_ok(s)) return fail(AA_EINVAL, "attn_bwd: strides must be multiples of 8");
+  if (!(a->softmax_scale > 0.f)) return fail(AA_EINVAL, "attn_bwd: softmax_scale must be > 0");
+  const bwd::WsLayout wl = bwd::ws_layout(a->B, a->Sq, a->Sk, a->H);
   const size_t need = aa_attn_bwd_workspace(a->B, a->Sq, a->Sk, a->H, a->hd);
   if (need > 0 && (!workspace || workspace_bytes < need))
     return fail(AA_EINVAL, "attn_bwd: workspace too small");
+  if (need > 0 && !aligned16(workspace))
+    return fail(AA_EINVAL, "attn_bwd: workspace must be 16-byte aligned");
 
   bwd::Params p;
   p.dout = (const bf16*)a->dout;
@@ -451,7 +539,6 @@ extern "C" int aa_attn_bwd(const aa_attn_bwd_args* a, void* workspace, size_t wo
   p.v = (const bf16*)a->v;
   p.o = (const bf16*)a->out;
   p.lse = a->lse;
-  p.delta = (float*)workspace;
   p.dq = (bf16*)a->dq;
   p.dk = (bf16*)a->dk;
   p.dv = (bf16*)a->dv;
@@ -465,27 +552,37 @@ extern "C" int aa_attn_bwd(const aa_attn_bwd_args* a, void* workspace, size_t wo
     p.s_dk[i] = a->dk_stride[i];
     p.s_dv[i] = a->dv_stride[i];
   }
+  char* ws = (char*)workspace;
+  p.qT = (bf16*)(ws + wl.qT);
+  p.doT = (bf16*)(ws + wl.doT);
+  p.kT = (bf16*)(ws + wl.kT);
+  p.stats = (float*)(ws + wl.stats);
   p.H = (int)a->H;
   p.Sq = (int)a->Sq;
   p.Sk = (int)a->Sk;
+  p.ntq = (int)((a->Sq + bwd::kT - 1) / bwd::kT);
+  p.ntk = (int)((a->Sk + bwd::kT - 1) / bwd::kT);
   p.scale = a->softmax_scale;
   p.c = a->softmax_scale * kLog2e;
   hipStream_t st = (hipStream_t)stream;
 
   const int64_t BH = a->B * a->H;
+  // Nothing reads the workspace when Sq == 0 (dK = dV = 0 and no dQ rows).
+  const int ntmax = p.ntq > p.ntk ? p.ntq : p.ntk;
   if (a->Sq > 0) {
-    const int64_t nrow = a->B * a->Sq * a->H;
-    bwd::rowdot_kernel<<<dim3((unsigned)((nrow * 16 + 255) / 256)), 256, 0, st>>>(p, nrow);
-    if (int rc = check_launch("attn_bwd rowdot")) return rc;
+    bwd::prep_kernel<<<dim3((unsigned)ntmax, (unsigned)a->H, (unsigned)a->B), 256, 0, st>>>(p);
+    if (int rc = check_launch("attn_bwd prep")) return rc;
   }
   if (a->Sk > 0) {
     const int nkblk = (int)((a->Sk + bwd::kKeysPerWg - 1) / bwd::kKeysPerWg);
-    bwd::dkdv_kernel<<<dim3((unsigned)(BH * nkblk)), 256, 0, st>>>(p, nkblk);
+    const int total = (int)(BH * nkblk);
+    bwd::dkdv_kernel<<<dim3((unsigned)total), 256, 0, st>>>(p, nkblk, total);
     if (int rc = check_launch("attn_bwd dkdv")) return rc;
   }
   if (a->Sq > 0) {
     const int nqblk = (int)((a->Sq + bwd::kQueriesPerWg - 1) / bwd::kQueriesPerWg);
-    bwd::dq_kernel<<<dim3((unsigned)(BH * nqblk)), 256, 0, st>>>(p, nqblk);
+    const int total = (int)(BH * nqblk);
+    bwd::dq_kernel<<<dim3((unsigned)total), 256, 0, st>>>(p, nqblk, total);
     if (int rc = check_launch("attn_bwd dq")) return rc;
   }
   return AA_OK;

@@ -4,41 +4,33 @@
 // Work decomposition
 //   One workgroup = 8 waves = 256 queries of one (batch, head). Each wave
 //   owns 32 queries for the whole kernel; K/V tiles of 64 keys are streamed
-//   into a 3-stage LDS ring and shared by the 8 waves. The waves run in two
+//   into a 4-stage LDS ring and shared by the 8 waves. The waves run in two
 //   phase-shifted groups so that MFMA and softmax work overlap on every SIMD
 //   (schedule at the kernel).
 //
 // Transposed formulation (per wave, per 64-key tile)
-//   S^T = K Q^T   : A = K rows from LDS (32 keys x 16 d per MFMA),
-//                   B = Q^T from registers (loaded once).
-//   O^T += V^T P^T: A = V^T (32 d x 16 keys) read from the row-major V tile
-//                   with ds_read_b64_tr_b16, B = P^T from the S^T accumulators.
+//   S^T = K Q^T   : A = K rows from the LDS row tile (32 keys x 16 d per
+//                   MFMA), B = Q^T from registers (loaded once).
+//   O^T += V^T P^T: A = V^T (32 d x 16 keys) from the LDS transposed tile,
+//                   B = P^T from the S^T accumulators.
 //   The 32x32 accumulator layout puts column j = lane%32 in every lane, with
 //   rows 8*(r/4) + 4*(lane/32) + r%4 in register r. With queries as columns,
 //   every lane holds one query: the softmax row max/sum are in-lane
 //   reductions plus one v_permlane32_swap with the partner lane, and the
 //   output rescale is a per-lane scalar multiply.
 //
-// K/V staging: global_load_lds_dwordx4 (DMA, no registers). A DMA instruction
-//   writes 64 lanes x 16 B contiguously (1 KB), so rows cannot be padded;
-//   instead the tile is stored as 256-byte slices of (16-row group, 16-byte
-//   chunk), with an XOR on the slot for V, so that both operand reads are
-//   free of bank conflicts on the 64 banks of 4 B (layout at the DMA code).
-//   The lane picks which global row/chunk it fetches so that the LDS side
-//   stays contiguous.
+// K/V staging (tile_io.h): K rows are copied HBM -> LDS by DMA
+//   (global_load_lds_dwordx4) into the row-tile layout. V is first written
+//   to HBM in the transposed tile format by vt_pack_kernel (one pass over V,
+//   16 KB per 64 keys), then copied linearly; both operand reads are 16-byte
+//   ds_read_b128 without bank conflicts.
 //
-// Transposed read (ds_read_b64_tr_b16): within each group of 16 lanes, lane i
-//   receives element (i & 3) of the 4 b16 values addressed by lanes
-//   4j + (i >> 2), j = 0..3. With source lane s pointing at
-//   V[k0 + (s >> 2)][d0 + 4 (s & 3)], lane i gets V[k0 + j][d0 + i], j = 0..3:
-//   4 keys of one d column, i.e. a row of V^T.
-//
-// Key permutation for P^T
+// Key order of P^T
 //   The B operand of the MFMA wants, in lane l, 8 consecutive k-indices
 //   8*(l/32)+i of a 16-key chunk. The S^T accumulators hold, for that lane,
 //   keys {4h..4h+3, 8+4h..8+4h+3} (h = l/32) of the chunk. Since PV sums over
-//   keys, the A operand is read in the same order: its elements 0-3 are keys
-//   4h..4h+3 and 4-7 are keys 8+4h..8+4h+3 (two transposed reads).
+//   keys, V^T only has to list its keys in the same order, which the
+//   transposed tile format does (tt_col in tile_io.h).
 //
 // Online softmax with lazy rescaling
 //   The running max m is tracked on raw scores s = q.k; probabilities are
@@ -51,13 +43,12 @@
 #include <cstdlib>
 #include <type_traits>
 
-#include "aa_common.h"
+#include "tile_io.h"
 
 namespace aa {
 
 constexpr int kD = 128;
 constexpr int kBN = 64;                     // keys per tile
-constexpr int kTileElems = kBN * kD;        // one K or V tile (16 KB)
 constexpr float kRescaleThreshold = 8.0f;   // log2 units
 
 struct FwdParams {
@@ -77,71 +68,20 @@ struct FwdParams {
   float c;  // softmax_scale * log2(e)
 };
 
-// V^T tile format (one 64-key tile = 8192 elements, 16 KB), the exact LDS
-// image the PV operand reads want:
-//   element (d, key) at (d >> 4) * 1024 + c' * 128 + (d & 15) * 8 + e,
-// where the tile's keys are taken in 16-key chunks c4 and, within a chunk,
-// in the order that matches the P^T accumulator layout: c' = 2 c4 + h holds
-// keys 16 c4 + 4 h + {0..3} (e = 0..3) and 16 c4 + 8 + 4 h + {0..3} (e = 4..7).
-// A wave's 16-byte read for (dt, c4) is then lane li, h = lane / 32:
-//   (li >> 4) * 1024 + h * 128 + (li & 15) * 8 + 2048 dt + 256 c4,
-// 16 consecutive 16-byte slots per 16 lanes: no bank conflicts.
-__device__ __forceinline__ int vt_key(int cp, int e) {
-  return 16 * (cp >> 1) + 8 * ((e >> 2) & 1) + 4 * (cp & 1) + (e & 3);
-}
-
-// One workgroup per (tile, head, batch): V rows [64 t, 64 t + 64) into LDS
-// (coalesced 16-byte loads, zero past Sk), then gathered into the V^T tile
-// format and written out with coalesced 16-byte stores.
+// V^T tiles: V in the transposed tile format (columns = keys, tile_io.h),
+// one 16 KB tile per 64 keys, written by vt_pack_kernel: one workgroup per
+// (tile, head, batch); zero past Sk.
 __global__ __launch_bounds__(256) void vt_pack_kernel(const bf16* __restrict__ v, int64_t vs0,
                                                       int64_t vs1, int64_t vs2, int Sk, int H,
                                                       int ntk, bf16* __restrict__ vt) {
-  constexpr int kRow = 128 + 8;  // padded LDS row (elements)
-  __shared__ __attribute__((aligned(16))) bf16 tile[64 * kRow];
+  __shared__ __attribute__((aligned(16))) bf16 stage[kTileRows * kPackRow];
   const int t = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-  const int tid = threadIdx.x;
-  const bf16* src = v + b * vs0 + h * vs2;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int id = tid + 256 * i;
-    const int row = id >> 4, dc = id & 15;
-    const int key = 64 * t + row;
-    u32x4 w = {0u, 0u, 0u, 0u};
-    if (key < Sk) w = ld16(src + (int64_t)key * vs1 + 8 * dc);
-    st16(tile + row * kRow + 8 * dc, w);
-  }
-  __syncthreads();
-  bf16* dst = vt + (((int64_t)b * H + h) * ntk + t) * 8192;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int oi = tid + 256 * i;  // 16-byte output chunk, in output order
-    const int d = 16 * (oi >> 7) + (oi & 15);
-    const int cp = (oi >> 4) & 7;
-    bf16x8 w;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) w[e] = tile[vt_key(cp, e) * kRow + d];
-    *reinterpret_cast<bf16x8*>(dst + 8 * oi) = w;
-  }
+  pack_transposed_tile(v + b * vs0 + h * vs2, vs1, kTileRows * t, Sk,
+                       vt + (((int64_t)b * H + h) * ntk + t) * kTileElems, stage);
 }
-
-typedef __attribute__((address_space(3))) void lds_void;
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-typedef short s16x8 __attribute__((ext_vector_type(8)));
-typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
-// Address-space casts keep the pointer's provenance (the __shared__ array it
-// points into), so the compiler can tell a DMA into one stage from reads of
-// the other and does not insert waits for the in-flight DMA before them.
-__device__ __forceinline__ lds_void* to_lds(const void* p) { return (lds_void*)p; }
-
-// Transposed LDS read: 4 bf16 per lane (lane mapping in the header).
-__device__ __forceinline__ s16x4 lds_read_tr(const bf16* p) {
-  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p);
-}
-
-__device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 // All but the newest n tiles of this wave's DMA complete (8 instructions per
 // tile for a group-A wave: 4 K + 4 V). n is wave-uniform, 0..3.
 __device__ __forceinline__ void wait_dma_tiles_in_flight(int n) {
@@ -151,17 +91,6 @@ __device__ __forceinline__ void wait_dma_tiles_in_flight(int n) {
     case 2: asm volatile("s_waitcnt vmcnt(16)" ::: "memory"); break;
     default: asm volatile("s_waitcnt vmcnt(24)" ::: "memory"); break;
   }
-}
-
-// 16 bytes per lane from global memory straight into LDS at
-// lds_base + 16 * lane (global_load_lds_dwordx4; M0 holds the LDS base).
-// Issued as inline asm so the compiler does not treat every later LDS read as
-// possibly depending on this write: completion is tracked by wait_dma() and
-// the workgroup barrier that follows it.
-__device__ __forceinline__ void dma16(const void* src, const void* lds_base) {
-  const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void*)lds_base);
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0)
-               : "memory", "m0");
 }
 
 constexpr int kWaves = 8;    // two groups of 4, one wave of each group per SIMD
@@ -187,13 +116,9 @@ void attn_fwd_kernel(FwdParams p) {
   constexpr int kDmaPerWave = 16 / kDmaWaves;  // 1 KB DMA blocks per group-A wave per tile, K and V each
   __shared__ __attribute__((aligned(1024))) bf16 kv_lds[kStages][2][kTileElems];
 
-  // Block -> (batch, head, query block). Workgroups are dispatched round-robin
-  // over the 8 XCDs; remap so each XCD gets a contiguous range of logical
-  // blocks, i.e. the same few heads, whose K/V then stay in that XCD's L2.
-  int logical = blockIdx.x;
-  if ((p.total_blocks & 7) == 0) {
-    logical = (blockIdx.x & 7) * (p.total_blocks >> 3) + (blockIdx.x >> 3);
-  }
+  // Block -> (batch, head, query block), XCD-aware: the query blocks of one
+  // head share an XCD and its L2.
+  const int logical = xcd_remap(blockIdx.x, p.total_blocks);
   const int qblk = logical % p.nqblk;
   const int bh = logical / p.nqblk;
   const int b = bh / p.H;
@@ -225,15 +150,10 @@ void attn_fwd_kernel(FwdParams p) {
   const bf16* kp = p.k + b * p.ks0 + h * p.ks2;
   const bf16* vp = p.v + b * p.vs0 + h * p.vs2;
 
-  // LDS tile layout (elements): row r, 16-byte chunk c of a 64 x 128 tile at
-  //   (r >> 4) * 2048 + c * 128 + slot(r, c) * 8, one 256-byte slice per
-  //   (16-row group, chunk). K: slot = r & 15 (the A-operand read of 16 lanes
-  //   covers 16 consecutive slots). V: slot = (r & 15) ^ 4 (c & 3) (a
-  //   transposed read of 32 lanes covers 4 rows x 4 chunks = 16 slots).
-  // A DMA instruction fills 1 KB = one 16-row group x 4 chunks; lane l writes
-  // slot l & 15 of chunk 4 (blk & 3) + (l >> 4), so it fetches row
-  // 16 (blk >> 2) + slot^-1 from global memory. Offsets are one per-lane base
-  // plus 32 elements per further block of the same wave.
+  // K: row tile (tile_io.h). A DMA instruction fills 1 KB = one 16-row group
+  // x 4 chunks; lane l writes slot l & 15 of chunk 4 (blk & 3) + (l >> 4), so
+  // it fetches row 16 (blk >> 2) + (l & 15). For a full tile the offsets are
+  // one per-lane base plus 32 elements per further block of the same wave.
   const int b0 = wave * kDmaPerWave;
   const int l15 = lane & 15, lq = lane >> 4;
   const int dma_krow = 16 * (b0 >> 2) + l15;
@@ -265,10 +185,10 @@ void attn_fwd_kernel(FwdParams p) {
   };
 
   // Per-lane LDS read bases (elements). K operand (kt, kk): row 32kt + li,
-  // chunk 2kk + hh -> k_rd + 4096 kt + 256 kk.
-  const int k_rd = (li >> 4) * 2048 + (li & 15) * 8 + hh * 128;
-  // V^T operand (dt, c4): v_rd + 2048 dt + 256 c4 (tile format above).
-  const int v_rd = (li >> 4) * 1024 + hh * 128 + (li & 15) * 8;
+  // chunk 2kk + hh -> k_rd + 4096 kt + 256 kk. V^T operand (dt, c4):
+  // v_rd + 2048 dt + 256 c4.
+  const int k_rd = row_rd(lane);
+  const int v_rd = tt_rd(lane);
 
   f32x16 o[4];
 #pragma unroll
