@@ -39,6 +39,9 @@ DEVICE_FLAGS = [
 ]
 
 
+RESOURCE_REMARK = "-Rpass-analysis=kernel-resource-usage"
+
+
 def hipcc() -> str:
     """Path of hipcc (ROCM_PATH/bin, then PATH)."""
     rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
@@ -51,6 +54,26 @@ def hipcc() -> str:
     return found
 
 
+def _check_resources(stderr: str, src: str) -> None:
+    """Fails the build if any kernel of `src` uses scratch memory or spills VGPRs.
+
+    The remarks come from -Rpass-analysis=kernel-resource-usage. Every kernel
+    here is written to keep its working set in registers and LDS; a spill
+    means an unroll or an indexing pattern went wrong, and costs an order of
+    magnitude in speed, so it is treated as a build error."""
+    name = None
+    for line in stderr.splitlines():
+        if "remark:" not in line:
+            continue
+        body = line.split("remark:", 1)[1].strip()
+        if body.startswith("Function Name:"):
+            name = body.split(":", 1)[1].split("[")[0].strip()
+        elif body.startswith("ScratchSize [bytes/lane]:") or body.startswith("VGPRs Spill:"):
+            value = int(body.split(":", 1)[1].split("[")[0])
+            if value != 0:
+                raise RuntimeError(f"{src}: kernel {name}: {body.split('[-R')[0].strip()}")
+
+
 def _run(cmd: list[str]) -> None:
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
@@ -59,6 +82,8 @@ def _run(cmd: list[str]) -> None:
             line for line in proc.stderr.splitlines() if "packed-fp32-ops" not in line
         )
         raise RuntimeError(f"command failed ({proc.returncode}): {' '.join(cmd)}\n{err}")
+    if RESOURCE_REMARK in cmd:
+        _check_resources(proc.stderr, cmd[cmd.index("-c") + 1])
 
 
 def build(verbose: bool = False) -> Path:
@@ -70,7 +95,7 @@ def build(verbose: bool = False) -> Path:
     for src in SOURCES:
         obj = BUILD / (Path(src).stem + ".o")
         objs.append(str(obj))
-        cmds.append([cc, *DEVICE_FLAGS, "-c", str(CSRC / src), "-o", str(obj)])
+        cmds.append([cc, *DEVICE_FLAGS, RESOURCE_REMARK, "-c", str(CSRC / src), "-o", str(obj)])
     workers = max(1, min(len(cmds), os.cpu_count() or 1, 8))
     with ThreadPoolExecutor(workers) as pool:
         for cmd, _ in zip(cmds, pool.map(_run, cmds)):

@@ -18,7 +18,7 @@
 //      dP = dO V^T       A = dO rows (LDS), B = V^T (registers)
 //      dV^T += dO^T P    A = dO^T (LDS),    B = P from the S accumulators
 //      dK^T += Q^T dZ    A = Q^T (LDS),     B = dZ from the accumulators
-// 3. dq_kernel: 4 waves x 32 queries per workgroup; streams 64-key tiles
+// 3. dq_kernel: 8 waves x 32 queries per workgroup; streams 64-key tiles
 //    (K rows, V rows, K^T: 48 KB, two stages). Queries are the columns:
 //      S^T = K Q^T, dP^T = V dO^T, dQ^T += K^T dZ^T.
 // The transposed tiles list their columns in the accumulator row order
@@ -205,14 +205,15 @@ void dkdv_kernel(Params p, int nkblk, int total_blocks) {
     const bf16* qt = tiles[st][2];
     const bf16* dot = tiles[st][3];
 
-    // One unrolled stream of 64 MFMAs, A operands read from LDS kQueue ops
-    // ahead (sched_barrier fences keep the order):
-    //   ops 0-31 : kk = i / 4, half hq = (i / 2) % 2;
-    //              even: S[hq] += Q rows x K^T, odd: dP[hq] += dO rows x V^T
-    //   ops 32-63: c4 = j / 8, dt = (j / 2) % 4 (j = i - 32);
-    //              even: dV^T[dt] += dO^T x P, odd: dK^T[dt] += Q^T x dZ
-    // P and dZ are formed between op 31 and op 32, while the first operands
-    // of the second half are already in flight.
+    // One unrolled stream of 64 MFMAs in four segments of 16, A operands read
+    // from LDS kQueue ops ahead (sched_barrier fences keep the order):
+    //   seg 0: S[0], dP[0]   (query half 0)        op = 2 kk + (dP ? 1 : 0)
+    //   seg 1: S[1], dP[1]   (query half 1)        + forms P, dZ of half 0
+    //   seg 2: dV^T, dK^T for chunks c4 = 0, 1     + forms P, dZ of half 1
+    //   seg 3: dV^T, dK^T for chunks c4 = 2, 3
+    //   (segments 2, 3: j = op - 32, c4 = j / 8, dt = (j / 2) % 4, odd = dK)
+    // The P/dZ VALU work of a half runs two registers per MFMA step inside
+    // the next segment, so it overlaps the matrix pipe.
     f32x16 s[2], dp[2];
 #pragma unroll
     for (int hq = 0; hq < 2; ++hq)
@@ -224,7 +225,7 @@ void dkdv_kernel(Params p, int nkblk, int total_blocks) {
     bf16x8 pb[4], zb[4];
     auto load_op = [&](int i) -> bf16x8 {
       if (i < 32) {
-        const int kk = i >> 2, hq = (i >> 1) & 1;
+        const int hq = i >> 4, kk = (i >> 1) & 7;
         return *reinterpret_cast<const bf16x8*>(((i & 1) ? dor : qr) + r_rd + 4096 * hq + 256 * kk);
       }
       const int j = i - 32, c4 = j >> 3, dt = (j >> 1) & 3;
@@ -232,7 +233,7 @@ void dkdv_kernel(Params p, int nkblk, int total_blocks) {
     };
     auto run_op = [&](int i, bf16x8 a) {
       if (i < 32) {
-        const int kk = i >> 2, hq = (i >> 1) & 1;
+        const int hq = i >> 4, kk = (i >> 1) & 7;
         if (i & 1) dp[hq] = mfma32(a, vreg[kk], dp[hq]);
         else s[hq] = mfma32(a, kreg[kk], s[hq]);
       } else {
@@ -241,41 +242,51 @@ void dkdv_kernel(Params p, int nkblk, int total_blocks) {
         else dv[dt] = mfma32(a, pb[c4], dv[dt]);
       }
     };
-    // P = exp2(S c - lse2[q]); dZ = P (dP - D[q]). Register r of half hq is
-    // query 32 hq + 8 (r >> 2) + 4 hh + (r & 3).
-    auto form_p_dz = [&]() {
+    // Softmax statistics of a half: lse2 and D for its 16 register rows.
+    // Register r of half hq is query 32 hq + 8 (r >> 2) + 4 hh + (r & 3).
+    f32x4 l2[4], dd[4];
+    auto load_stats = [&](int hq) {
 #pragma unroll
-      for (int hq = 0; hq < 2; ++hq) {
+      for (int rq = 0; rq < 4; ++rq) {
+        const int q0 = 32 * hq + 8 * rq + 4 * hh;
+        l2[rq] = *reinterpret_cast<const f32x4*>(&stat[st][q0]);
+        dd[rq] = *reinterpret_cast<const f32x4*>(&stat[st][kT + q0]);
+      }
+    };
+    // P = exp2(S c - lse2[q]), dZ = P (dP - D[q]) for registers r, r + 1.
+    auto form2 = [&](int hq, int r) {
 #pragma unroll
-        for (int rq = 0; rq < 4; ++rq) {
-          const int q0 = 32 * hq + 8 * rq + 4 * hh;
-          const f32x4 l2 = *reinterpret_cast<const f32x4*>(&stat[st][q0]);
-          const f32x4 dd = *reinterpret_cast<const f32x4*>(&stat[st][kT + q0]);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int r = 4 * rq + i;
-            const float pv = fast_exp2(fmaf(s[hq][r], c, -l2[i]));
-            const float zv = pv * (dp[hq][r] - dd[i]);
-            const int c4 = 2 * hq + (r >> 3);
-            pb[c4][r & 7] = (bf16)pv;
-            zb[c4][r & 7] = (bf16)zv;
-          }
-        }
+      for (int e = 0; e < 2; ++e) {
+        const int rr = r + e;
+        const float pv = fast_exp2(fmaf(s[hq][rr], c, -l2[rr >> 2][rr & 3]));
+        const float zv = pv * (dp[hq][rr] - dd[rr >> 2][rr & 3]);
+        const int c4 = 2 * hq + (rr >> 3);
+        pb[c4][rr & 7] = (bf16)pv;
+        zb[c4][rr & 7] = (bf16)zv;
       }
     };
     bf16x8 queue[kQueue];
     auto step = [&](int i) {  // run op i - kQueue, then load op i into its slot
       const int u = i - kQueue;
       if (u >= 0) run_op(u, queue[u % kQueue]);
+      // Forming half h runs with ops 16 (h + 1) + 2 m, m = 0..7.
+      if (u >= 16 && u < 48 && (u & 1) == 0) form2((u - 16) >> 4, (u - 16) & 15);
+      if (u == 15) load_stats(0);
+      if (u == 31) load_stats(1);
       if (i < 64) queue[i % kQueue] = load_op(i);
       if ((i & 3) == 1 && (i >> 2) < 16 && more) issue_block(t + 1, st ^ 1, i >> 2);
       __builtin_amdgcn_sched_barrier(0);
     };
+    // Separate loops per segment: one 72-step loop is past the unroller's
+    // limit and would leave the queue in scratch memory.
 #pragma unroll
-    for (int i = 0; i < 32 + kQueue; ++i) step(i);
-    form_p_dz();
+    for (int i = 0; i < 16 + kQueue; ++i) step(i);
 #pragma unroll
-    for (int i = 32 + kQueue; i < 64 + kQueue; ++i) step(i);
+    for (int i = 16 + kQueue; i < 32 + kQueue; ++i) step(i);
+#pragma unroll
+    for (int i = 32 + kQueue; i < 48 + kQueue; ++i) step(i);
+#pragma unroll
+    for (int i = 48 + kQueue; i < 64 + kQueue; ++i) step(i);
 
     wait_dma();
     __syncthreads();
@@ -302,9 +313,14 @@ void dkdv_kernel(Params p, int nkblk, int total_blocks) {
 
 // ------------------------------------------------------------------ dQ --
 
-constexpr int kQueriesPerWg = 128;  // 4 waves x 32 queries
+constexpr int kDqWaves = 8;                  // two per SIMD
+constexpr int kDqQueue = 6;                  // operand queue depth (register-bound at 2 waves/SIMD)
+constexpr int kQueriesPerWg = kDqWaves * 32;
+constexpr int kDqBlocks = 16 / kDqWaves;     // DMA blocks per wave of each streamed tile
+constexpr int kDqDma = 3 * kDqBlocks;        // DMA instructions per wave per key tile
+constexpr int kDqDmaGap = 48 / kDqDma;       // MFMA steps between two of them
 
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+__global__ __launch_bounds__(kDqWaves * 64) __attribute__((amdgpu_waves_per_eu(kDqWaves / 4, kDqWaves / 4)))
 void dq_kernel(Params p, int nqblk, int total_blocks) {
   // Per stage: K rows, V rows (row tiles), K^T (transposed tile).
   __shared__ __attribute__((aligned(1024))) bf16 tiles[2][3][kTileElems];
@@ -348,11 +364,12 @@ void dq_kernel(Params p, int nqblk, int total_blocks) {
   const bf16* kTb = p.kT + (int64_t)bh * p.ntk * kTileElems;
   const int ntiles = p.ntk;
 
-  // Wave DMA j = 0..11: tile j / 4 (K rows, V rows, K^T), block 4 wave + j % 4.
+  // Wave DMA j = 0..kDqDma-1: tile j / kDqBlocks (K rows, V rows, K^T),
+  // block kDqBlocks * wave + j % kDqBlocks.
   auto issue_block = [&](int t, int st, int j) {
-    const int blk = 4 * wave + (j & 3);
+    const int blk = kDqBlocks * wave + (j % kDqBlocks);
     const int k0 = t * kT;
-    switch (j >> 2) {
+    switch (j / kDqBlocks) {
       case 0:
         dma_row_block(kbase + (int64_t)k0 * p.s_k[1], p.s_k[1], min(kT, p.Sk - k0), tiles[st][0],
                       blk, lane);
@@ -379,20 +396,20 @@ void dq_kernel(Params p, int nqblk, int total_blocks) {
 
   if (ntiles > 0) {
 #pragma unroll
-    for (int j = 0; j < 12; ++j) issue_block(0, 0, j);
+    for (int j = 0; j < kDqDma; ++j) issue_block(0, 0, j);
     wait_dma();
   }
   __syncthreads();
 
   for (int t = 0; t < ntiles; ++t) {
     const int st = t & 1;
-    // Tile t+1 into the other stage, its 12 DMA spread over the MFMA stream.
+    // Tile t+1 into the other stage, its DMA spread over the MFMA stream.
     const bool more = t + 1 < ntiles;
     const bf16* kr = tiles[st][0];
     const bf16* vr = tiles[st][1];
     const bf16* kt = tiles[st][2];
 
-    // One unrolled stream of 48 MFMAs with a kQueue-deep operand queue:
+    // One unrolled stream of 48 MFMAs with a kDqQueue-deep operand queue:
     //   ops 0-31 : kk = i / 4, half hk = (i / 2) % 2;
     //              even: S^T[hk] += K rows x Q^T, odd: dP^T[hk] += V rows x dO^T
     //   ops 32-47: c4 = j / 4, dt = j % 4 (j = i - 32): dQ^T[dt] += K^T x dZ^T
@@ -438,19 +455,19 @@ void dq_kernel(Params p, int nqblk, int total_blocks) {
         }
       }
     };
-    bf16x8 queue[kQueue];
-    auto step = [&](int i) {  // run op i - kQueue, then load op i into its slot
-      const int u = i - kQueue;
-      if (u >= 0) run_op(u, queue[u % kQueue]);
-      if (i < 48) queue[i % kQueue] = load_op(i);
-      if ((i & 3) == 1 && (i >> 2) < 12 && more) issue_block(t + 1, st ^ 1, i >> 2);
+    bf16x8 queue[kDqQueue];
+    auto step = [&](int i) {  // run op i - kDqQueue, then load op i into its slot
+      const int u = i - kDqQueue;
+      if (u >= 0) run_op(u, queue[u % kDqQueue]);
+      if (i < 48) queue[i % kDqQueue] = load_op(i);
+      if (i % kDqDmaGap == 1 && i / kDqDmaGap < kDqDma && more) issue_block(t + 1, st ^ 1, i / kDqDmaGap);
       __builtin_amdgcn_sched_barrier(0);
     };
 #pragma unroll
-    for (int i = 0; i < 32 + kQueue; ++i) step(i);
+    for (int i = 0; i < 32 + kDqQueue; ++i) step(i);
     form_dz();
 #pragma unroll
-    for (int i = 32 + kQueue; i < 48 + kQueue; ++i) step(i);
+    for (int i = 32 + kDqQueue; i < 48 + kDqQueue; ++i) step(i);
 
     wait_dma();
     __syncthreads();
@@ -582,7 +599,7 @@ extern "C" int aa_attn_bwd(const aa_attn_bwd_args* a, void* workspace, size_t wo
   if (a->Sq > 0) {
     const int nqblk = (int)((a->Sq + bwd::kQueriesPerWg - 1) / bwd::kQueriesPerWg);
     const int total = (int)(BH * nqblk);
-    bwd::dq_kernel<<<dim3((unsigned)total), 256, 0, st>>>(p, nqblk, total);
+    bwd::dq_kernel<<<dim3((unsigned)total), bwd::kDqWaves * 64, 0, st>>>(p, nqblk, total);
     if (int rc = check_launch("attn_bwd dq")) return rc;
   }
   return AA_OK;
