@@ -11,9 +11,10 @@
 //    transposed tiles Q^T, dO^T (columns = queries) and K^T (columns = keys)
 //    in the tile_io.h format, and per 64-query tile a 1 KB record of
 //    lse * log2(e) and D.
-// 2. dkdv_kernel: 4 waves x 32 keys per workgroup; streams 64-query tiles
-//    (Q rows, dO rows, Q^T, dO^T, stats: 65 KB, two stages) into LDS by DMA.
-//    Keys are the accumulator columns (lane % 32), K and V sit in registers:
+// 2. dkdv_kernel: 8 waves, 128 keys per workgroup (32 per wave pair, split
+//    by role at the kernel); streams 64-query tiles (Q rows, dO rows, Q^T,
+//    dO^T, stats: 65 KB, two stages) into LDS by DMA. Keys are the
+//    accumulator columns (lane % 32), K and V sit in registers:
 //      S  = Q K^T        A = Q rows (LDS),  B = K^T (registers)
 //      dP = dO V^T       A = dO rows (LDS), B = V^T (registers)
 //      dV^T += dO^T P    A = dO^T (LDS),    B = P from the S accumulators
@@ -101,14 +102,29 @@ __global__ __launch_bounds__(256) void prep_kernel(Params p) {
 
 // ------------------------------------------------------------ dK, dV --
 
-constexpr int kKeysPerWg = 128;  // 4 waves x 32 keys
-constexpr int kQueue = 8;        // LDS operands in flight ahead of the MFMA that uses them
+// 8 waves; pair w (waves w and w + 4, which share SIMD w) owns keys
+// 32 w .. 32 w + 31 of the workgroup's 128 and splits the work by role. Per
+// 64-query tile, with a workgroup barrier after each phase:
+//   phase 1: A (wave w)     S = Q K^T (16 MFMA); P = exp2(S c - lse2), written
+//                           as bf16 B operands to the pair's LDS slot
+//            B (wave w + 4) dP = dO V^T (16 MFMA)
+//   phase 2: A              dV^T += dO^T P (16 MFMA)
+//            B              P from the slot, dZ = P (dP - D), dK^T += Q^T dZ
+//                           (16 MFMA)
+// Every SIMD runs two waves of 16 MFMAs per phase, and one wave's VALU work
+// overlaps the other's MFMAs. A holds K and dV^T, B holds V and dK^T, so each
+// fits in half the register file.
+constexpr int kKeysPerWg = 128;
+constexpr int kDkWaves = 8;
+constexpr int kDkQueue = 8;                  // LDS operands in flight per wave
+constexpr int kDkDma = 64 / kDkWaves;        // 1 KB DMA blocks per wave per query tile
 
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+__global__ __launch_bounds__(kDkWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void dkdv_kernel(Params p, int nkblk, int total_blocks) {
   // Per stage: Q rows, dO rows (row tiles), Q^T, dO^T (transposed tiles).
   __shared__ __attribute__((aligned(1024))) bf16 tiles[2][4][kTileElems];
   __shared__ __attribute__((aligned(1024))) float stat[2][kStat];
+  __shared__ __attribute__((aligned(1024))) bf16x8 pslot[4][4][64];  // [pair][c4][lane]
 
   const int logical = xcd_remap(blockIdx.x, total_blocks);
   const int kblk = logical % nkblk;
@@ -116,25 +132,24 @@ void dkdv_kernel(Params p, int nkblk, int total_blocks) {
   const int b = bh / p.H, h = bh - (bh / p.H) * p.H;
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int pair = wave & 3;
+  const bool role_a = wave < 4;
   const int lane = tid & 63;
   const int li = lane & 31, hh = lane >> 5;
 
-  // K^T / V^T operands: lane holds K[key][16 kk + 8 hh + 0..7].
-  const int key = kblk * kKeysPerWg + wave * 32 + li;
+  // B operand of the role's first product: lane holds K (A) or V (B)
+  // [key][16 kk + 8 hh + 0..7].
+  const int key = kblk * kKeysPerWg + pair * 32 + li;
   const bool key_ok = key < p.Sk;
-  bf16x8 kreg[8], vreg[8];
+  bf16x8 kv[8];
   {
-    const bf16* kp = p.k + b * p.s_k[0] + h * p.s_k[2] + (int64_t)key * p.s_k[1] + 8 * hh;
-    const bf16* vp = p.v + b * p.s_v[0] + h * p.s_v[2] + (int64_t)key * p.s_v[1] + 8 * hh;
+    const bf16* src = role_a ? p.k + b * p.s_k[0] + h * p.s_k[2] + (int64_t)key * p.s_k[1]
+                             : p.v + b * p.s_v[0] + h * p.s_v[2] + (int64_t)key * p.s_v[1];
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk) {
-      u32x4 a = {0u, 0u, 0u, 0u}, c = {0u, 0u, 0u, 0u};
-      if (key_ok) {
-        a = ld16(kp + 16 * kk);
-        c = ld16(vp + 16 * kk);
-      }
-      kreg[kk] = as_bf16x8(a);
-      vreg[kk] = as_bf16x8(c);
+      u32x4 w = {0u, 0u, 0u, 0u};
+      if (key_ok) w = ld16(src + 8 * hh + 16 * kk);
+      kv[kk] = as_bf16x8(w);
     }
   }
 
@@ -145,12 +160,12 @@ void dkdv_kernel(Params p, int nkblk, int total_blocks) {
   const float* statb = p.stats + (int64_t)bh * p.ntq * kStat;
   const int ntiles = p.ntq;
 
-  // Each wave copies 4 of the 16 blocks of each of the 4 tiles (its DMA
-  // j = 0..15: tile j / 4, block 4 wave + j % 4); wave 0 also the stats.
+  // Wave DMA j = 0..7: tile j / 2 (Q rows, dO rows, Q^T, dO^T), block
+  // 2 wave + j % 2; wave 0 also copies the stats record.
   auto issue_block = [&](int t, int st, int j) {
-    const int blk = 4 * wave + (j & 3);
+    const int blk = 2 * wave + (j & 1);
     const int q0 = t * kT;
-    switch (j >> 2) {
+    switch (j >> 1) {
       case 0:
         dma_row_block(qbase + (int64_t)q0 * p.s_q[1], p.s_q[1], min(kT, p.Sq - q0), tiles[st][0],
                       blk, lane);
@@ -175,18 +190,15 @@ void dkdv_kernel(Params p, int nkblk, int total_blocks) {
   const int t_rd = tt_rd(lane);
   const float c = p.c;
 
-  f32x16 dk[4], dv[4];
+  f32x16 acc[4];  // dV^T (A) or dK^T (B)
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      dk[i][r] = 0.f;
-      dv[i][r] = 0.f;
-    }
+    for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
 
   if (ntiles > 0) {
 #pragma unroll
-    for (int j = 0; j < 16; ++j) issue_block(0, 0, j);
+    for (int j = 0; j < kDkDma; ++j) issue_block(0, 0, j);
     issue_stats(0, 0);
     wait_dma();
   }
@@ -195,117 +207,101 @@ void dkdv_kernel(Params p, int nkblk, int total_blocks) {
   for (int t = 0; t < ntiles; ++t) {
     const int st = t & 1;
     // Tile t+1 goes to the other stage, which held tile t-1 (all its reads
-    // ended before the last barrier). Its 16 DMA instructions are spread over
-    // the MFMA stream, one every 4 ops: issued back to back they stall the
-    // wave while the CU's address path drains them.
+    // ended before the last barrier); four DMA per phase, spread over the
+    // MFMA stream.
     const bool more = t + 1 < ntiles;
     if (more) issue_stats(t + 1, st ^ 1);
-    const bf16* qr = tiles[st][0];
-    const bf16* dor = tiles[st][1];
-    const bf16* qt = tiles[st][2];
-    const bf16* dot = tiles[st][3];
 
-    // One unrolled stream of 64 MFMAs in four segments of 16, A operands read
-    // from LDS kQueue ops ahead (sched_barrier fences keep the order):
-    //   seg 0: S[0], dP[0]   (query half 0)        op = 2 kk + (dP ? 1 : 0)
-    //   seg 1: S[1], dP[1]   (query half 1)        + forms P, dZ of half 0
-    //   seg 2: dV^T, dK^T for chunks c4 = 0, 1     + forms P, dZ of half 1
-    //   seg 3: dV^T, dK^T for chunks c4 = 2, 3
-    //   (segments 2, 3: j = op - 32, c4 = j / 8, dt = (j / 2) % 4, odd = dK)
-    // The P/dZ VALU work of a half runs two registers per MFMA step inside
-    // the next segment, so it overlaps the matrix pipe.
-    f32x16 s[2], dp[2];
+    // 16 MFMAs fed by a kDkQueue-deep queue of LDS operands.
+    auto stream16 = [&](auto load_op, auto run_op, int dma0) {
+      bf16x8 queue[kDkQueue];
+#pragma unroll
+      for (int i = 0; i < 16 + kDkQueue; ++i) {
+        const int u = i - kDkQueue;
+        if (u >= 0) run_op(u, queue[u % kDkQueue]);
+        if (i < 16) queue[i % kDkQueue] = load_op(i);
+        if ((i & 3) == 1 && (i >> 2) < 4 && more) issue_block(t + 1, st ^ 1, dma0 + (i >> 2));
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    };
+
+    // Phase 1: x = S (A) or dP (B) for the two 32-query halves; op i:
+    // half i / 8, kk = i % 8. Register r of half hq is query
+    // 32 hq + 8 (r >> 2) + 4 hh + (r & 3).
+    f32x16 x[2];
 #pragma unroll
     for (int hq = 0; hq < 2; ++hq)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        s[hq][r] = 0.f;
-        dp[hq][r] = 0.f;
-      }
-    bf16x8 pb[4], zb[4];
-    auto load_op = [&](int i) -> bf16x8 {
-      if (i < 32) {
-        const int hq = i >> 4, kk = (i >> 1) & 7;
-        return *reinterpret_cast<const bf16x8*>(((i & 1) ? dor : qr) + r_rd + 4096 * hq + 256 * kk);
-      }
-      const int j = i - 32, c4 = j >> 3, dt = (j >> 1) & 3;
-      return *reinterpret_cast<const bf16x8*>(((j & 1) ? qt : dot) + t_rd + 2048 * dt + 256 * c4);
-    };
-    auto run_op = [&](int i, bf16x8 a) {
-      if (i < 32) {
-        const int hq = i >> 4, kk = (i >> 1) & 7;
-        if (i & 1) dp[hq] = mfma32(a, vreg[kk], dp[hq]);
-        else s[hq] = mfma32(a, kreg[kk], s[hq]);
-      } else {
-        const int j = i - 32, c4 = j >> 3, dt = (j >> 1) & 3;
-        if (j & 1) dk[dt] = mfma32(a, zb[c4], dk[dt]);
-        else dv[dt] = mfma32(a, pb[c4], dv[dt]);
-      }
-    };
-    // Softmax statistics of a half: lse2 and D for its 16 register rows.
-    // Register r of half hq is query 32 hq + 8 (r >> 2) + 4 hh + (r & 3).
-    f32x4 l2[4], dd[4];
-    auto load_stats = [&](int hq) {
+      for (int r = 0; r < 16; ++r) x[hq][r] = 0.f;
+    {
+      const bf16* rows = tiles[st][role_a ? 0 : 1];
+      stream16(
+          [&](int i) {
+            return *reinterpret_cast<const bf16x8*>(rows + r_rd + 4096 * (i >> 3) + 256 * (i & 7));
+          },
+          [&](int i, bf16x8 a) { x[i >> 3] = mfma32(a, kv[i & 7], x[i >> 3]); }, 0);
+    }
+    bf16x8 bop[4];  // B operands of phase 2: P (A) or dZ (B)
+    if (role_a) {
 #pragma unroll
-      for (int rq = 0; rq < 4; ++rq) {
-        const int q0 = 32 * hq + 8 * rq + 4 * hh;
-        l2[rq] = *reinterpret_cast<const f32x4*>(&stat[st][q0]);
-        dd[rq] = *reinterpret_cast<const f32x4*>(&stat[st][kT + q0]);
-      }
-    };
-    // P = exp2(S c - lse2[q]), dZ = P (dP - D[q]) for registers r, r + 1.
-    auto form2 = [&](int hq, int r) {
+      for (int hq = 0; hq < 2; ++hq)
 #pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const int rr = r + e;
-        const float pv = fast_exp2(fmaf(s[hq][rr], c, -l2[rr >> 2][rr & 3]));
-        const float zv = pv * (dp[hq][rr] - dd[rr >> 2][rr & 3]);
-        const int c4 = 2 * hq + (rr >> 3);
-        pb[c4][rr & 7] = (bf16)pv;
-        zb[c4][rr & 7] = (bf16)zv;
-      }
-    };
-    bf16x8 queue[kQueue];
-    auto step = [&](int i) {  // run op i - kQueue, then load op i into its slot
-      const int u = i - kQueue;
-      if (u >= 0) run_op(u, queue[u % kQueue]);
-      // Forming half h runs with ops 16 (h + 1) + 2 m, m = 0..7.
-      if (u >= 16 && u < 48 && (u & 1) == 0) form2((u - 16) >> 4, (u - 16) & 15);
-      if (u == 15) load_stats(0);
-      if (u == 31) load_stats(1);
-      if (i < 64) queue[i % kQueue] = load_op(i);
-      if ((i & 3) == 1 && (i >> 2) < 16 && more) issue_block(t + 1, st ^ 1, i >> 2);
-      __builtin_amdgcn_sched_barrier(0);
-    };
-    // Separate loops per segment: one 72-step loop is past the unroller's
-    // limit and would leave the queue in scratch memory.
+        for (int rq = 0; rq < 4; ++rq) {
+          const f32x4 l2 = *reinterpret_cast<const f32x4*>(&stat[st][32 * hq + 8 * rq + 4 * hh]);
 #pragma unroll
-    for (int i = 0; i < 16 + kQueue; ++i) step(i);
+          for (int i = 0; i < 4; ++i) {
+            const int r = 4 * rq + i;
+            bop[2 * hq + (r >> 3)][r & 7] = (bf16)fast_exp2(fmaf(x[hq][r], c, -l2[i]));
+          }
+        }
 #pragma unroll
-    for (int i = 16 + kQueue; i < 32 + kQueue; ++i) step(i);
-#pragma unroll
-    for (int i = 32 + kQueue; i < 48 + kQueue; ++i) step(i);
-#pragma unroll
-    for (int i = 48 + kQueue; i < 64 + kQueue; ++i) step(i);
+      for (int c4 = 0; c4 < 4; ++c4) pslot[pair][c4][lane] = bop[c4];
+    }
+    __syncthreads();
 
+    // Phase 2: acc[dt] += T(dt, c4) x bop[c4], T = dO^T (A) or Q^T (B); op i:
+    // c4 = i / 4, dt = i % 4.
+    if (!role_a) {
+#pragma unroll
+      for (int c4 = 0; c4 < 4; ++c4) bop[c4] = pslot[pair][c4][lane];
+#pragma unroll
+      for (int hq = 0; hq < 2; ++hq)
+#pragma unroll
+        for (int rq = 0; rq < 4; ++rq) {
+          const f32x4 dd = *reinterpret_cast<const f32x4*>(&stat[st][kT + 32 * hq + 8 * rq + 4 * hh]);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int r = 4 * rq + i;
+            const int c4 = 2 * hq + (r >> 3);
+            bop[c4][r & 7] = (bf16)((float)bop[c4][r & 7] * (x[hq][r] - dd[i]));
+          }
+        }
+    }
+    {
+      const bf16* tt = tiles[st][role_a ? 3 : 2];
+      stream16(
+          [&](int i) {
+            return *reinterpret_cast<const bf16x8*>(tt + t_rd + 2048 * (i & 3) + 256 * (i >> 2));
+          },
+          [&](int i, bf16x8 a) { acc[i & 3] = mfma32(a, bop[i >> 2], acc[i & 3]); }, 4);
+    }
     wait_dma();
     __syncthreads();
   }
 
   if (key_ok) {
-    bf16* dkp = p.dk + b * p.s_dk[0] + (int64_t)key * p.s_dk[1] + h * p.s_dk[2] + 4 * hh;
-    bf16* dvp = p.dv + b * p.s_dv[0] + (int64_t)key * p.s_dv[1] + h * p.s_dv[2] + 4 * hh;
+    bf16* dst = role_a ? p.dv + b * p.s_dv[0] + (int64_t)key * p.s_dv[1] + h * p.s_dv[2]
+                       : p.dk + b * p.s_dk[0] + (int64_t)key * p.s_dk[1] + h * p.s_dk[2];
+    const float sc = role_a ? 1.0f : p.scale;
+    dst += 4 * hh;
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) {
 #pragma unroll
       for (int rq = 0; rq < 4; ++rq) {
-        const f32x16& a = dk[dt];
-        const f32x16& e = dv[dt];
-        u32x2 wk = {pack_bf16(a[4 * rq] * p.scale, a[4 * rq + 1] * p.scale),
-                    pack_bf16(a[4 * rq + 2] * p.scale, a[4 * rq + 3] * p.scale)};
-        u32x2 wv = {pack_bf16(e[4 * rq], e[4 * rq + 1]), pack_bf16(e[4 * rq + 2], e[4 * rq + 3])};
-        *reinterpret_cast<u32x2*>(dkp + 32 * dt + 8 * rq) = wk;
-        *reinterpret_cast<u32x2*>(dvp + 32 * dt + 8 * rq) = wv;
+        const f32x16& a = acc[dt];
+        u32x2 w = {pack_bf16(a[4 * rq] * sc, a[4 * rq + 1] * sc),
+                   pack_bf16(a[4 * rq + 2] * sc, a[4 * rq + 3] * sc)};
+        *reinterpret_cast<u32x2*>(dst + 32 * dt + 8 * rq) = w;
       }
     }
   }
@@ -593,7 +589,7 @@ extern "C" int aa_attn_bwd(const aa_attn_bwd_args* a, void* workspace, size_t wo
   if (a->Sk > 0) {
     const int nkblk = (int)((a->Sk + bwd::kKeysPerWg - 1) / bwd::kKeysPerWg);
     const int total = (int)(BH * nkblk);
-    bwd::dkdv_kernel<<<dim3((unsigned)total), 256, 0, st>>>(p, nkblk, total);
+    bwd::dkdv_kernel<<<dim3((unsigned)total), bwd::kDkWaves * 64, 0, st>>>(p, nkblk, total);
     if (int rc = check_launch("attn_bwd dkdv")) return rc;
   }
   if (a->Sq > 0) {
