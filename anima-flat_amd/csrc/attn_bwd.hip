@@ -8,12 +8,12 @@
 //
 // Three kernels:
 // 1. prep_kernel, one workgroup per (64-row tile, head, batch): writes the
-//    transposed tiles Q^T, dO^T (columns = queries) and K^T (columns = keys)
-//    in the tile_io.h format, and per 64-query tile a 1 KB record of
-//    lse * log2(e) and D.
+//    transposed K^T tiles (columns = keys) in the tile_io.h format, and per
+//    64-query tile a 1 KB record of lse * log2(e) and -D.
 // 2. dkdv_kernel: 8 waves, 128 keys per workgroup (32 per wave pair, split
-//    by role at the kernel); streams 64-query tiles (Q rows, dO rows, Q^T,
-//    dO^T, stats: 65 KB, two stages) into LDS by DMA. Keys are the
+//    by role, the roles one phase apart, at the kernel); streams 64-query
+//    tiles (Q rows, dO rows, stats: 33 KB) into LDS by DMA and reads Q^T and
+//    dO^T from the same rows with transposed LDS reads. Keys are the
 //    accumulator columns (lane % 32), K and V sit in registers:
 //      S  = Q K^T        A = Q rows (LDS),  B = K^T (registers)
 //      dP = dO V^T       A = dO rows (LDS), B = V^T (registers)
@@ -32,7 +32,7 @@ namespace bwd {
 
 constexpr int kD = 128;
 constexpr int kT = kTileRows;  // rows (queries or keys) per streamed tile
-constexpr int kStat = 256;     // floats per 64-query stats record: lse2[64], D[64], zero pad
+constexpr int kStat = 256;     // floats per 64-query stats record: lse2[64], -D[64], zero pad
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
@@ -47,8 +47,6 @@ struct Params {
   bf16* dk;
   bf16* dv;
   int64_t s_do[3], s_q[3], s_k[3], s_v[3], s_o[3], s_dq[3], s_dk[3], s_dv[3];
-  bf16* qT;      // [B][H][ntq][8192] transposed Q tiles
-  bf16* doT;     // [B][H][ntq][8192] transposed dO tiles
   bf16* kT;      // [B][H][ntk][8192] transposed K tiles
   float* stats;  // [B][H][ntq][kStat]
   int H, Sq, Sk, ntq, ntk;
@@ -65,10 +63,6 @@ __global__ __launch_bounds__(256) void prep_kernel(Params p) {
   const int tid = threadIdx.x;
   if (t < p.ntq) {
     const int q0 = t * kT;
-    pack_transposed_tile(p.q + b * p.s_q[0] + h * p.s_q[2], p.s_q[1], q0, p.Sq,
-                         p.qT + (bh * p.ntq + t) * kTileElems, stage);
-    pack_transposed_tile(p.dout + b * p.s_do[0] + h * p.s_do[2], p.s_do[1], q0, p.Sq,
-                         p.doT + (bh * p.ntq + t) * kTileElems, stage);
     // D = rowsum(dO * O): 4 lanes per row, 32 values each. Rows past Sq get
     // lse2 = +inf (P = 0) and D = 0.
     const int row = tid >> 2, part = tid & 3;
@@ -90,7 +84,7 @@ __global__ __launch_bounds__(256) void prep_kernel(Params p) {
     float* st = p.stats + (bh * p.ntq + t) * kStat;
     if (part == 0) {
       st[row] = q < p.Sq ? p.lse[bh * p.Sq + q] * kLog2e : INFINITY;
-      st[kT + row] = d;
+      st[kT + row] = -d;
     }
     if (tid < kStat - 2 * kT) st[2 * kT + tid] = 0.f;
   }
@@ -103,27 +97,45 @@ __global__ __launch_bounds__(256) void prep_kernel(Params p) {
 // ------------------------------------------------------------ dK, dV --
 
 // 8 waves; pair w (waves w and w + 4, which share SIMD w) owns keys
-// 32 w .. 32 w + 31 of the workgroup's 128 and splits the work by role. Per
-// 64-query tile, with a workgroup barrier after each phase:
-//   phase 1: A (wave w)     S = Q K^T (16 MFMA); P = exp2(S c - lse2), written
-//                           as bf16 B operands to the pair's LDS slot
-//            B (wave w + 4) dP = dO V^T (16 MFMA)
-//   phase 2: A              dV^T += dO^T P (16 MFMA)
-//            B              P from the slot, dZ = P (dP - D), dK^T += Q^T dZ
-//                           (16 MFMA)
-// Every SIMD runs two waves of 16 MFMAs per phase, and one wave's VALU work
-// overlaps the other's MFMAs. A holds K and dV^T, B holds V and dK^T, so each
-// fits in half the register file.
+// 32 w .. 32 w + 31 of the workgroup's 128 and splits the work by role:
+// A (wave w) holds K and accumulates dV^T, B (wave w + 4) holds V and
+// accumulates dK^T. Per 64-query tile t each role runs one MFMA block and one
+// VALU block:
+//   A: M_A(t) = dV^T += dO^T_{t-1} P_{t-1} (16) and S_t = Q_t K^T (16)
+//      X_A(t) = P_t = exp2(S_t c - lse2_t) -> bf16 B operands, copied to the
+//               pair's LDS slot for B
+//   B: M_B(t) = dK^T += Q^T_{t-1} dZ_{t-1} (16) and dP_t - D_t = dO_t V^T (16,
+//               accumulators start at -D_t)
+//      X_B(t) = dZ_t = P_t o (dP_t - D_t) (P_t from the slot)
+// The two roles run the same instruction stream one phase apart (B executes
+// one extra barrier first, A one at the end), with a workgroup barrier
+// between phases:
+//   phase 2t   : A runs M_A(t), B runs X_B(t-1)
+//   phase 2t+1 : A runs X_A(t), B runs M_B(t)
+// so on every SIMD one wave's MFMAs overlap the other wave's VALU work.
+// Only the Q and dO rows of each query tile come into LDS (swizzled row
+// tiles, tile_io.h) with its stats record, in a 4-stage ring: the S / dP A
+// operands are 16-byte row reads, the dV / dK A operands (dO^T, Q^T of the
+// previous tile) are pairs of ds_read_b64_tr_b16 transposed reads of the same
+// tiles. The B waves DMA tile t+2 at the start of X_B(t-1) (phase 2t); it is
+// complete at the end of phase 2t+3.
 constexpr int kKeysPerWg = 128;
 constexpr int kDkWaves = 8;
-constexpr int kDkQueue = 8;                  // LDS operands in flight per wave
-constexpr int kDkDma = 64 / kDkWaves;        // 1 KB DMA blocks per wave per query tile
+constexpr int kDkQueue = 8;   // A operands in flight per wave
+constexpr int kDkStages = 4;  // query tiles in the LDS ring
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// Transposed read: 4 bf16 per lane (tile_io.h swizzled row tile layout).
+__device__ __forceinline__ s16x4 ds_read_tr(const bf16* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(lds_void*)p);
+}
 
 __global__ __launch_bounds__(kDkWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void dkdv_kernel(Params p, int nkblk, int total_blocks) {
-  // Per stage: Q rows, dO rows (row tiles), Q^T, dO^T (transposed tiles).
-  __shared__ __attribute__((aligned(1024))) bf16 tiles[2][4][kTileElems];
-  __shared__ __attribute__((aligned(1024))) float stat[2][kStat];
+  __shared__ __attribute__((aligned(1024))) bf16 rows[kDkStages][2][kTileElems];  // [stage][Q, dO]
+  __shared__ __attribute__((aligned(1024))) float stat[kDkStages][kStat];
   __shared__ __attribute__((aligned(1024))) bf16x8 pslot[4][4][64];  // [pair][c4][lane]
 
   const int logical = xcd_remap(blockIdx.x, total_blocks);
@@ -137,7 +149,7 @@ void dkdv_kernel(Params p, int nkblk, int total_blocks) {
   const int lane = tid & 63;
   const int li = lane & 31, hh = lane >> 5;
 
-  // B operand of the role's first product: lane holds K (A) or V (B)
+  // B operand of the role's S / dP product: lane holds K (A) or V (B)
   // [key][16 kk + 8 hh + 0..7].
   const int key = kblk * kKeysPerWg + pair * 32 + li;
   const bool key_ok = key < p.Sk;
@@ -155,39 +167,38 @@ void dkdv_kernel(Params p, int nkblk, int total_blocks) {
 
   const bf16* qbase = p.q + b * p.s_q[0] + h * p.s_q[2];
   const bf16* dobase = p.dout + b * p.s_do[0] + h * p.s_do[2];
-  const bf16* qTb = p.qT + (int64_t)bh * p.ntq * kTileElems;
-  const bf16* doTb = p.doT + (int64_t)bh * p.ntq * kTileElems;
   const float* statb = p.stats + (int64_t)bh * p.ntq * kStat;
   const int ntiles = p.ntq;
 
-  // Wave DMA j = 0..7: tile j / 2 (Q rows, dO rows, Q^T, dO^T), block
-  // 2 wave + j % 2; wave 0 also copies the stats record.
-  auto issue_block = [&](int t, int st, int j) {
-    const int blk = 2 * wave + (j & 1);
-    const int q0 = t * kT;
-    switch (j >> 1) {
-      case 0:
-        dma_row_block(qbase + (int64_t)q0 * p.s_q[1], p.s_q[1], min(kT, p.Sq - q0), tiles[st][0],
-                      blk, lane);
-        break;
-      case 1:
-        dma_row_block(dobase + (int64_t)q0 * p.s_do[1], p.s_do[1], min(kT, p.Sq - q0),
-                      tiles[st][1], blk, lane);
-        break;
-      case 2:
-        dma16(qTb + (int64_t)t * kTileElems + blk * 512 + lane * 8, tiles[st][2] + blk * 512);
-        break;
-      default:
-        dma16(doTb + (int64_t)t * kTileElems + blk * 512 + lane * 8, tiles[st][3] + blk * 512);
-        break;
-    }
-  };
-  auto issue_stats = [&](int t, int st) {
-    if (wave == 0) dma16(statb + (int64_t)t * kStat + 4 * lane, stat[st]);
+  // DMA by the B waves, g = wave - 4: blocks 4 g .. 4 g + 3 of the Q and dO
+  // row tiles; wave 4 also copies the stats record (kTileDma instructions).
+  const int g4 = 4 * (wave & 3);
+  auto issue_tile = [&](int t) {
+    const int st = t % kDkStages, q0 = t * kT, nr = min(kT, p.Sq - q0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      dma_row_block_swz(qbase + (int64_t)q0 * p.s_q[1], p.s_q[1], nr, rows[st][0], g4 + i, lane);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      dma_row_block_swz(dobase + (int64_t)q0 * p.s_do[1], p.s_do[1], nr, rows[st][1], g4 + i, lane);
+    if (wave == 4) dma16(statb + (int64_t)t * kStat + 4 * lane, stat[st]);
   };
 
-  const int r_rd = row_rd(lane);
-  const int t_rd = tt_rd(lane);
+  // Per-lane read offsets (elements) in a swizzled row tile.
+  // Row operand of op (hq, kk) = row 32 hq + li, chunk 2 kk + hh: slot
+  // (li & 15) ^ 4 (2 (kk & 1) + hh); base rs[kk & 1], + 4096 hq + 256 kk.
+  const int rs0 = (li >> 4) * 2048 + hh * 128 + (((li & 15) ^ (4 * hh)) * 8);
+  const int rs1 = (li >> 4) * 2048 + hh * 128 + (((li & 15) ^ (8 + 4 * hh)) * 8);
+  // Transposed operand of op (c4, dt), lane 16 G + 4 j + c: two reads r2 =
+  // 0, 1 of rows (queries) 16 c4 + 4 (G >> 1) + j + 8 r2, columns 32 dt +
+  // 16 (G & 1) + 4 c .. + 3; lane 16 G + i receives column 32 dt + 16 (G & 1)
+  // + i of those four rows, i.e. A[d][k] with k = 8 (G >> 1) + 4 r2 + j, the
+  // query order of the P / dZ B operands. Base tb[r2], + 2048 c4 + 512 dt.
+  const int G = lane >> 4, tj = (lane >> 2) & 3, tc = lane & 3;
+  const int tbase = 256 * (G & 1) + 128 * (tc >> 1) + 4 * (tc & 1) +
+                    8 * (((4 * (G >> 1) + tj) ^ (4 * (tc >> 1))) & 7);
+  const int tb0 = tbase + 64 * (G & 1);
+  const int tb1 = tbase + 64 * (1 - (G & 1));
   const float c = p.c;
 
   f32x16 acc[4];  // dV^T (A) or dK^T (B)
@@ -195,59 +206,71 @@ void dkdv_kernel(Params p, int nkblk, int total_blocks) {
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
+  f32x16 x[2];    // S_t (A) or dP_t - D_t (B); register r of half hq is query
+                  // 32 hq + 8 (r >> 2) + 4 hh + (r & 3)
+  bf16x8 bop[4];  // P_{t-1} (A) or dZ_{t-1} (B), B operands of the next M block
 
-  if (ntiles > 0) {
-#pragma unroll
-    for (int j = 0; j < kDkDma; ++j) issue_block(0, 0, j);
-    issue_stats(0, 0);
-    wait_dma();
-  }
-  __syncthreads();
-
-  for (int t = 0; t < ntiles; ++t) {
-    const int st = t & 1;
-    // Tile t+1 goes to the other stage, which held tile t-1 (all its reads
-    // ended before the last barrier); four DMA per phase, spread over the
-    // MFMA stream.
-    const bool more = t + 1 < ntiles;
-    if (more) issue_stats(t + 1, st ^ 1);
-
-    // 16 MFMAs fed by a kDkQueue-deep queue of LDS operands.
-    auto stream16 = [&](auto load_op, auto run_op, int dma0) {
-      bf16x8 queue[kDkQueue];
-#pragma unroll
-      for (int i = 0; i < 16 + kDkQueue; ++i) {
-        const int u = i - kDkQueue;
-        if (u >= 0) run_op(u, queue[u % kDkQueue]);
-        if (i < 16) queue[i % kDkQueue] = load_op(i);
-        if ((i & 3) == 1 && (i >> 2) < 4 && more) issue_block(t + 1, st ^ 1, dma0 + (i >> 2));
-        __builtin_amdgcn_sched_barrier(0);
-      }
-    };
-
-    // Phase 1: x = S (A) or dP (B) for the two 32-query halves; op i:
-    // half i / 8, kk = i % 8. Register r of half hq is query
-    // 32 hq + 8 (r >> 2) + 4 hh + (r & 3).
-    f32x16 x[2];
-#pragma unroll
-    for (int hq = 0; hq < 2; ++hq)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) x[hq][r] = 0.f;
-    {
-      const bf16* rows = tiles[st][role_a ? 0 : 1];
-      stream16(
-          [&](int i) {
-            return *reinterpret_cast<const bf16x8*>(rows + r_rd + 4096 * (i >> 3) + 256 * (i & 7));
-          },
-          [&](int i, bf16x8 a) { x[i >> 3] = mfma32(a, kv[i & 7], x[i >> 3]); }, 0);
-    }
-    bf16x8 bop[4];  // B operands of phase 2: P (A) or dZ (B)
-    if (role_a) {
+  // M block of tile t: ops 0-15 (PV) acc[dt] += T_{t-1}(dt, c4) bop[c4] with
+  // c4 = op / 4, dt = op % 4; ops 16-31 (QK) x[hq] += R_t(hq, kk) kv[kk] with
+  // hq = (op - 16) / 8, kk = op % 8. T = dO^T (A) or Q^T (B), read transposed
+  // from the previous tile's dO / Q rows; R = Q rows (A) or dO rows (B). x
+  // starts at 0 (A: the zero pad of the stats record) or -D_t (B). One
+  // unrolled stream fed by a kDkQueue-deep operand queue.
+  auto mblock = [&](int t, auto pv_tag, auto qk_tag) {
+    constexpr bool PV = decltype(pv_tag)::value;
+    constexpr bool QK = decltype(qk_tag)::value;
+    constexpr int first = PV ? 0 : 16;
+    constexpr int last = QK ? 32 : 16;
+    const bf16* tt = rows[(t + kDkStages - 1) % kDkStages][role_a ? 1 : 0];
+    const bf16* rr = rows[t % kDkStages][role_a ? 0 : 1];
+    if constexpr (QK) {
+      const float* init = stat[t % kDkStages] + (role_a ? 2 * kT : kT);
 #pragma unroll
       for (int hq = 0; hq < 2; ++hq)
 #pragma unroll
         for (int rq = 0; rq < 4; ++rq) {
-          const f32x4 l2 = *reinterpret_cast<const f32x4*>(&stat[st][32 * hq + 8 * rq + 4 * hh]);
+          const f32x4 v4 = *reinterpret_cast<const f32x4*>(init + 32 * hq + 8 * rq + 4 * hh);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) x[hq][4 * rq + i] = v4[i];
+        }
+    }
+    auto load_op = [&](int op) -> bf16x8 {
+      if (op < 16) {
+        const bf16* base = tt + 2048 * (op >> 2) + 512 * (op & 3);
+        const s16x4 lo = ds_read_tr(base + tb0);
+        const s16x4 hi = ds_read_tr(base + tb1);
+        return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+      }
+      const int w = op - 16;
+      return *reinterpret_cast<const bf16x8*>(rr + ((w & 1) ? rs1 : rs0) + 4096 * (w >> 3) +
+                                               256 * (w & 7));
+    };
+    auto run_op = [&](int op, bf16x8 a) {
+      if (op < 16) {
+        acc[op & 3] = mfma32(a, bop[op >> 2], acc[op & 3]);
+      } else {
+        const int w = op - 16;
+        x[w >> 3] = mfma32(a, kv[w & 7], x[w >> 3]);
+      }
+    };
+    bf16x8 queue[kDkQueue];
+#pragma unroll
+    for (int i = first; i < last + kDkQueue; ++i) {
+      if (i - kDkQueue >= first) run_op(i - kDkQueue, queue[(i - kDkQueue - first) % kDkQueue]);
+      if (i < last) queue[(i - first) % kDkQueue] = load_op(i);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  // X block of tile t (B first copies tile t + 3).
+  auto xblock = [&](int t) {
+    if (role_a) {
+      const float* l2p = stat[t % kDkStages];
+#pragma unroll
+      for (int hq = 0; hq < 2; ++hq)
+#pragma unroll
+        for (int rq = 0; rq < 4; ++rq) {
+          const f32x4 l2 = *reinterpret_cast<const f32x4*>(l2p + 32 * hq + 8 * rq + 4 * hh);
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int r = 4 * rq + i;
@@ -256,37 +279,58 @@ void dkdv_kernel(Params p, int nkblk, int total_blocks) {
         }
 #pragma unroll
       for (int c4 = 0; c4 < 4; ++c4) pslot[pair][c4][lane] = bop[c4];
-    }
-    __syncthreads();
-
-    // Phase 2: acc[dt] += T(dt, c4) x bop[c4], T = dO^T (A) or Q^T (B); op i:
-    // c4 = i / 4, dt = i % 4.
-    if (!role_a) {
+    } else {
+      if (t + 3 < ntiles) issue_tile(t + 3);
 #pragma unroll
       for (int c4 = 0; c4 < 4; ++c4) bop[c4] = pslot[pair][c4][lane];
 #pragma unroll
       for (int hq = 0; hq < 2; ++hq)
 #pragma unroll
-        for (int rq = 0; rq < 4; ++rq) {
-          const f32x4 dd = *reinterpret_cast<const f32x4*>(&stat[st][kT + 32 * hq + 8 * rq + 4 * hh]);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int r = 4 * rq + i;
-            const int c4 = 2 * hq + (r >> 3);
-            bop[c4][r & 7] = (bf16)((float)bop[c4][r & 7] * (x[hq][r] - dd[i]));
-          }
+        for (int r = 0; r < 16; ++r) {
+          const int c4 = 2 * hq + (r >> 3);
+          bop[c4][r & 7] = (bf16)((float)bop[c4][r & 7] * x[hq][r]);
         }
     }
-    {
-      const bf16* tt = tiles[st][role_a ? 3 : 2];
-      stream16(
-          [&](int i) {
-            return *reinterpret_cast<const bf16x8*>(tt + t_rd + 2048 * (i & 3) + 256 * (i >> 2));
-          },
-          [&](int i, bf16x8 a) { acc[i & 3] = mfma32(a, bop[i >> 2], acc[i & 3]); }, 4);
+  };
+
+  // Stages: tile t in t % 4, written at phase 2t-4 (the stage of tile t-4,
+  // whose last reads were in phase 2t-5), read in phases 2t .. 2t+3. At the
+  // end of M_B(t) (phase 2t+1) a B wave waits for tile t+1; tile t+2 may be in
+  // flight.
+  const int tile_dma = wave == 4 ? 9 : 8;  // DMA instructions per tile (B waves)
+  auto wait_tile_next = [&](int t) {
+    if (t + 2 < ntiles) {
+      if (tile_dma == 9) asm volatile("s_waitcnt vmcnt(9)" ::: "memory");
+      else asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    } else {
+      wait_dma();
     }
+  };
+  if (ntiles > 0 && !role_a) {
+    issue_tile(0);
     wait_dma();
+  }
+  __syncthreads();
+  if (ntiles > 0) {
+    if (!role_a) {  // the DMA of X_B(-2) and X_B(-1), then the phase shift
+      if (1 < ntiles) issue_tile(1);
+      if (2 < ntiles) issue_tile(2);
+      __syncthreads();
+    }
+    mblock(0, std::false_type{}, std::true_type{});
+    if (!role_a) wait_tile_next(0);
     __syncthreads();
+    xblock(0);
+    __syncthreads();
+    for (int t = 1; t < ntiles; ++t) {
+      mblock(t, std::true_type{}, std::true_type{});
+      if (!role_a) wait_tile_next(t);
+      __syncthreads();
+      xblock(t);
+      __syncthreads();
+    }
+    mblock(ntiles, std::true_type{}, std::false_type{});
+    if (role_a) __syncthreads();
   }
 
   if (key_ok) {
@@ -348,11 +392,11 @@ void dq_kernel(Params p, int nqblk, int total_blocks) {
       doreg[kk] = as_bf16x8(e);
     }
   }
-  float lse2 = INFINITY, dlt = 0.f;
+  float lse2 = INFINITY, ndlt = 0.f;  // -D
   if (q_ok) {
     const float* st = p.stats + ((int64_t)bh * p.ntq + qrow / kT) * kStat + (qrow % kT);
     lse2 = st[0];
-    dlt = st[kT];
+    ndlt = st[kT];
   }
 
   const bf16* kbase = p.k + b * p.s_k[0] + h * p.s_k[2];
@@ -447,7 +491,7 @@ void dq_kernel(Params p, int nqblk, int total_blocks) {
         for (int r = 0; r < 16; ++r) {
           float pv = fast_exp2(fmaf(s[hk][r], c, -lse2));
           if (partial && kb + 32 * hk + 8 * (r >> 2) + 4 * hh + (r & 3) >= p.Sk) pv = 0.f;
-          zb[2 * hk + (r >> 3)][r & 7] = (bf16)(pv * (dp[hk][r] - dlt));
+          zb[2 * hk + (r >> 3)][r & 7] = (bf16)(pv * (dp[hk][r] + ndlt));
         }
       }
     };
@@ -490,16 +534,14 @@ static bool stride_ok(const int64_t* s) {
 }
 
 struct WsLayout {
-  size_t qT, doT, kT, stats, total;
+  size_t kT, stats, total;
 };
 
 static WsLayout ws_layout(int64_t B, int64_t Sq, int64_t Sk, int64_t H) {
   const int64_t ntq = (Sq + kT - 1) / kT, ntk = (Sk + kT - 1) / kT;
   const size_t tile = (size_t)kTileElems * sizeof(bf16);
   WsLayout w;
-  w.qT = 0;
-  w.doT = w.qT + (size_t)(B * H * ntq) * tile;
-  w.kT = w.doT + (size_t)(B * H * ntq) * tile;
+  w.kT = 0;
   w.stats = w.kT + (size_t)(B * H * ntk) * tile;
   w.total = w.stats + (size_t)(B * H * ntq) * kStat * sizeof(float);
   return w;
@@ -566,8 +608,6 @@ extern "C" int aa_attn_bwd(const aa_attn_bwd_args* a, void* workspace, size_t wo
     p.s_dv[i] = a->dv_stride[i];
   }
   char* ws = (char*)workspace;
-  p.qT = (bf16*)(ws + wl.qT);
-  p.doT = (bf16*)(ws + wl.doT);
   p.kT = (bf16*)(ws + wl.kT);
   p.stats = (float*)(ws + wl.stats);
   p.H = (int)a->H;

@@ -121,6 +121,20 @@ __device__ __forceinline__ void dma_row_block(const bf16* base, int64_t rs, int 
   dma16(base + (int64_t)row * rs + 8 * chunk, lds_tile + blk * 512);
 }
 
+// Swizzled row tile (dK/dV kernel): element (r, d) at
+//   (r >> 4) * 2048 + (d >> 3) * 128 + (((r & 15) ^ (4 * ((d >> 3) & 3))) * 8) + (d & 7),
+// i.e. the row tile with the row slot inside each 256-byte slice XORed with
+// 4 * (chunk % 4). Row-operand reads (16 rows of one chunk per 16 lanes) stay
+// conflict free, and so do transposed reads with ds_read_b64_tr_b16 (4 rows x
+// 4 chunks per 32 lanes land in 16 distinct slots). One DMA block blk holds
+// rows 16 (blk >> 2) + ((lane & 15) ^ (4 (lane >> 4))), chunk 4 (blk & 3) + (lane >> 4).
+__device__ __forceinline__ void dma_row_block_swz(const bf16* base, int64_t rs, int nrows,
+                                                  const bf16* lds_tile, int blk, int lane) {
+  const int row = min(16 * (blk >> 2) + ((lane & 15) ^ (4 * (lane >> 4))), nrows - 1);
+  const int chunk = 4 * (blk & 3) + (lane >> 4);
+  dma16(base + (int64_t)row * rs + 8 * chunk, lds_tile + blk * 512);
+}
+
 // DMA blocks [b0, b0 + N) of a tile stored contiguously (16 KB) at `src`.
 template <int N>
 __device__ __forceinline__ void dma_linear_tile(const bf16* src, const bf16* lds_tile, int b0,

@@ -287,9 +287,11 @@ def main() -> int:
         qg, kg, vg = (t.detach().clone().requires_grad_(True) for t in (q, k, v.contiguous()))
         dout = torch.randn(B, S, H * d, device=dev, dtype=BF)
 
+        # torch.autograd.grad returns dq, dk, dv without accumulating them into
+        # .grad (no extra elementwise adds in the timed region).
         def fwd_bwd():
             out = pkg.attention(qg, kg, vg)
-            out.backward(dout)
+            torch.autograd.grad(out, (qg, kg, vg), dout)
 
         _, us_fb = time_launches(fwd_bwd, max(5, steps // 2), 2)
         fb_flops = 3.5 * flops

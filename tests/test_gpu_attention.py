@@ -169,6 +169,7 @@ def test_config3_masked_full(pkg):
         (1, 256, 256, 2),
         (2, 100, 77, 3),  # partial tiles on both sides
         (1, 64, 300, 1),
+        (1, 150, 200, 2),  # three query tiles
         (1, 1024, 1024, 4),
     ],
 )
