@@ -7,9 +7,8 @@
 //   dK = scale * dZ^T Q, dQ = scale * dZ K.
 //
 // Three kernels:
-// 1. prep_kernel, one workgroup per (64-row tile, head, batch): writes the
-//    transposed K^T tiles (columns = keys) in the tile_io.h format, and per
-//    64-query tile a 1 KB record of lse * log2(e) and -D.
+// 1. prep_kernel, one workgroup per (64-query tile, head, batch): writes a
+//    1 KB record of lse * log2(e) and -D per 64 queries.
 // 2. dkdv_kernel: 8 waves, 128 keys per workgroup (32 per wave pair, split
 //    by role, the roles one phase apart, at the kernel); streams 64-query
 //    tiles (Q rows, dO rows, stats: 33 KB) into LDS by DMA and reads Q^T and
@@ -19,11 +18,13 @@
 //      dP = dO V^T       A = dO rows (LDS), B = V^T (registers)
 //      dV^T += dO^T P    A = dO^T (LDS),    B = P from the S accumulators
 //      dK^T += Q^T dZ    A = Q^T (LDS),     B = dZ from the accumulators
-// 3. dq_kernel: 8 waves x 32 queries per workgroup; streams 64-key tiles
-//    (K rows, V rows, K^T: 48 KB, two stages). Queries are the columns:
+// 3. dq_kernel: 8 waves x 32 queries per workgroup, two groups one phase
+//    apart; streams 64-key tiles (K rows, V rows: 32 KB) and reads K^T from
+//    the K rows with transposed LDS reads. Queries are the columns:
 //      S^T = K Q^T, dP^T = V dO^T, dQ^T += K^T dZ^T.
-// The transposed tiles list their columns in the accumulator row order
-// (tt_col), so the bf16-rounded accumulators are the B operands as they are.
+// The transposed reads list the keys / queries of each 16-column chunk in the
+// accumulator row order, so the bf16-rounded accumulators are the B operands
+// as they are.
 #include "tile_io.h"
 
 namespace aa {
@@ -47,7 +48,6 @@ struct Params {
   bf16* dk;
   bf16* dv;
   int64_t s_do[3], s_q[3], s_k[3], s_v[3], s_o[3], s_dq[3], s_dk[3], s_dv[3];
-  bf16* kT;      // [B][H][ntk][8192] transposed K tiles
   float* stats;  // [B][H][ntq][kStat]
   int H, Sq, Sk, ntq, ntk;
   float c;      // scale * log2(e)
@@ -57,41 +57,34 @@ struct Params {
 // ---------------------------------------------------------------- prep --
 
 __global__ __launch_bounds__(256) void prep_kernel(Params p) {
-  __shared__ __attribute__((aligned(16))) bf16 stage[kT * kPackRow];
   const int t = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int64_t bh = (int64_t)b * p.H + h;
   const int tid = threadIdx.x;
-  if (t < p.ntq) {
-    const int q0 = t * kT;
-    // D = rowsum(dO * O): 4 lanes per row, 32 values each. Rows past Sq get
-    // lse2 = +inf (P = 0) and D = 0.
-    const int row = tid >> 2, part = tid & 3;
-    const int q = q0 + row;
-    float d = 0.f;
-    if (q < p.Sq) {
-      const bf16* dop = p.dout + b * p.s_do[0] + (int64_t)q * p.s_do[1] + h * p.s_do[2] + 32 * part;
-      const bf16* op = p.o + b * p.s_o[0] + (int64_t)q * p.s_o[1] + h * p.s_o[2] + 32 * part;
+  const int q0 = t * kT;
+  // D = rowsum(dO * O): 4 lanes per row, 32 values each. Rows past Sq get
+  // lse2 = +inf (P = 0) and D = 0.
+  const int row = tid >> 2, part = tid & 3;
+  const int q = q0 + row;
+  float d = 0.f;
+  if (q < p.Sq) {
+    const bf16* dop = p.dout + b * p.s_do[0] + (int64_t)q * p.s_do[1] + h * p.s_do[2] + 32 * part;
+    const bf16* op = p.o + b * p.s_o[0] + (int64_t)q * p.s_o[1] + h * p.s_o[2] + 32 * part;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        float x[8], y[8];
-        unpack8(ld16(dop + 8 * j), x);
-        unpack8(ld16(op + 8 * j), y);
+    for (int j = 0; j < 4; ++j) {
+      float x[8], y[8];
+      unpack8(ld16(dop + 8 * j), x);
+      unpack8(ld16(op + 8 * j), y);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) d = fmaf(x[i], y[i], d);
-      }
+      for (int i = 0; i < 8; ++i) d = fmaf(x[i], y[i], d);
     }
-    d = group_sum<4>(d);
-    float* st = p.stats + (bh * p.ntq + t) * kStat;
-    if (part == 0) {
-      st[row] = q < p.Sq ? p.lse[bh * p.Sq + q] * kLog2e : INFINITY;
-      st[kT + row] = -d;
-    }
-    if (tid < kStat - 2 * kT) st[2 * kT + tid] = 0.f;
   }
-  if (t < p.ntk) {
-    pack_transposed_tile(p.k + b * p.s_k[0] + h * p.s_k[2], p.s_k[1], t * kT, p.Sk,
-                         p.kT + (bh * p.ntk + t) * kTileElems, stage);
+  d = group_sum<4>(d);
+  float* st = p.stats + (bh * p.ntq + t) * kStat;
+  if (part == 0) {
+    st[row] = q < p.Sq ? p.lse[bh * p.Sq + q] * kLog2e : INFINITY;
+    st[kT + row] = -d;
   }
+  if (tid < kStat - 2 * kT) st[2 * kT + tid] = 0.f;
 }
 
 // ------------------------------------------------------------ dK, dV --
@@ -353,17 +346,26 @@ void dkdv_kernel(Params p, int nkblk, int total_blocks) {
 
 // ------------------------------------------------------------------ dQ --
 
+// 8 waves x 32 queries (256 per workgroup), Q^T and dO^T in registers; keys
+// are the accumulator rows. Per 64-key tile t a wave runs
+//   M(t): dQ^T += K^T_{t-1} dZ^T_{t-1} (16 MFMA; K^T read transposed from the
+//         K rows of tile t-1), S^T_t = K_t Q^T (16), dP^T_t - D = V_t dO^T
+//         (16, accumulators start at -D)
+//   X(t): dZ^T_t = exp2(S^T_t c - lse2) o (dP^T_t - D) as bf16 B operands.
+// Waves 0-3 (group A) and 4-7 (group B) run the same stream one phase apart
+// (B executes one extra barrier first, A one at the end):
+//   phase 2t: A runs M(t), B runs X(t-1);  phase 2t+1: A runs X(t), B runs M(t)
+// K and V rows stream into a 4-stage ring of swizzled row tiles (tile_io.h):
+// group A DMAs tile t+2 at the start of X(t) (phase 2t+1) into the stage of
+// tile t-2 (last read in phase 2t-1) and waits for tile t+1 at its end.
 constexpr int kDqWaves = 8;                  // two per SIMD
 constexpr int kDqQueue = 6;                  // operand queue depth (register-bound at 2 waves/SIMD)
+constexpr int kDqStages = 4;
 constexpr int kQueriesPerWg = kDqWaves * 32;
-constexpr int kDqBlocks = 16 / kDqWaves;     // DMA blocks per wave of each streamed tile
-constexpr int kDqDma = 3 * kDqBlocks;        // DMA instructions per wave per key tile
-constexpr int kDqDmaGap = 48 / kDqDma;       // MFMA steps between two of them
 
-__global__ __launch_bounds__(kDqWaves * 64) __attribute__((amdgpu_waves_per_eu(kDqWaves / 4, kDqWaves / 4)))
+__global__ __launch_bounds__(kDqWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void dq_kernel(Params p, int nqblk, int total_blocks) {
-  // Per stage: K rows, V rows (row tiles), K^T (transposed tile).
-  __shared__ __attribute__((aligned(1024))) bf16 tiles[2][3][kTileElems];
+  __shared__ __attribute__((aligned(1024))) bf16 tiles[kDqStages][2][kTileElems];  // [stage][K, V]
 
   const int logical = xcd_remap(blockIdx.x, total_blocks);
   const int qblk = logical % nqblk;
@@ -371,6 +373,7 @@ void dq_kernel(Params p, int nqblk, int total_blocks) {
   const int b = bh / p.H, h = bh - (bh / p.H) * p.H;
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool group_a = wave < 4;
   const int lane = tid & 63;
   const int li = lane & 31, hh = lane >> 5;
 
@@ -401,31 +404,30 @@ void dq_kernel(Params p, int nqblk, int total_blocks) {
 
   const bf16* kbase = p.k + b * p.s_k[0] + h * p.s_k[2];
   const bf16* vbase = p.v + b * p.s_v[0] + h * p.s_v[2];
-  const bf16* kTb = p.kT + (int64_t)bh * p.ntk * kTileElems;
   const int ntiles = p.ntk;
 
-  // Wave DMA j = 0..kDqDma-1: tile j / kDqBlocks (K rows, V rows, K^T),
-  // block kDqBlocks * wave + j % kDqBlocks.
-  auto issue_block = [&](int t, int st, int j) {
-    const int blk = kDqBlocks * wave + (j % kDqBlocks);
-    const int k0 = t * kT;
-    switch (j / kDqBlocks) {
-      case 0:
-        dma_row_block(kbase + (int64_t)k0 * p.s_k[1], p.s_k[1], min(kT, p.Sk - k0), tiles[st][0],
-                      blk, lane);
-        break;
-      case 1:
-        dma_row_block(vbase + (int64_t)k0 * p.s_v[1], p.s_v[1], min(kT, p.Sk - k0), tiles[st][1],
-                      blk, lane);
-        break;
-      default:
-        dma16(kTb + (int64_t)t * kTileElems + blk * 512 + lane * 8, tiles[st][2] + blk * 512);
-        break;
-    }
+  // DMA by group A, g = wave: blocks 4 g .. 4 g + 3 of the K and V row tiles.
+  const int g4 = 4 * (wave & 3);
+  auto issue_tile = [&](int t) {
+    const int st = t % kDqStages, k0 = t * kT, nr = min(kT, p.Sk - k0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      dma_row_block_swz(kbase + (int64_t)k0 * p.s_k[1], p.s_k[1], nr, tiles[st][0], g4 + i, lane);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      dma_row_block_swz(vbase + (int64_t)k0 * p.s_v[1], p.s_v[1], nr, tiles[st][1], g4 + i, lane);
   };
 
-  const int r_rd = row_rd(lane);
-  const int t_rd = tt_rd(lane);
+  // Read offsets in the swizzled row tiles, as in dkdv_kernel: row operands
+  // (row 32 hk + li, chunk 2 kk + hh) at rs[kk & 1] + 4096 hk + 256 kk;
+  // transposed operands (c4, dt) at tb[r2] + 2048 c4 + 512 dt.
+  const int rs0 = (li >> 4) * 2048 + hh * 128 + (((li & 15) ^ (4 * hh)) * 8);
+  const int rs1 = (li >> 4) * 2048 + hh * 128 + (((li & 15) ^ (8 + 4 * hh)) * 8);
+  const int G = lane >> 4, tj = (lane >> 2) & 3, tc = lane & 3;
+  const int tbase = 256 * (G & 1) + 128 * (tc >> 1) + 4 * (tc & 1) +
+                    8 * (((4 * (G >> 1) + tj) ^ (4 * (tc >> 1))) & 7);
+  const int tb0 = tbase + 64 * (G & 1);
+  const int tb1 = tbase + 64 * (1 - (G & 1));
   const float c = p.c;
 
   f32x16 dq[4];
@@ -433,85 +435,111 @@ void dq_kernel(Params p, int nqblk, int total_blocks) {
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int r = 0; r < 16; ++r) dq[i][r] = 0.f;
+  // S^T and dP^T - D of the tile between its M and X blocks; register r of
+  // half hk is key 32 hk + 8 (r >> 2) + 4 hh + (r & 3) of the tile.
+  f32x16 s[2], dp[2];
+  bf16x8 zb[4];  // dZ^T of the previous tile, B operands of the next M block
 
-  if (ntiles > 0) {
+  // M block of tile t, one unrolled stream of up to 48 MFMAs fed by a
+  // kDqQueue-deep operand queue:
+  //   ops 0-15 : c4 = op / 4, dt = op % 4: dQ^T[dt] += K^T_{t-1}(dt, c4) zb[c4]
+  //   ops 16-47: w = op - 16, kk = w / 4, hk = (w / 2) % 2;
+  //              even w: S^T[hk] += K_t rows x Q^T, odd w: dP^T[hk] += V_t rows x dO^T
+  auto mblock = [&](int t, auto pv_tag, auto qk_tag) {
+    constexpr bool PV = decltype(pv_tag)::value;
+    constexpr bool QK = decltype(qk_tag)::value;
+    constexpr int first = PV ? 0 : 16;
+    constexpr int last = QK ? 48 : 16;
+    const bf16* kprev = tiles[(t + kDqStages - 1) % kDqStages][0];
+    const bf16* kr = tiles[t % kDqStages][0];
+    const bf16* vr = tiles[t % kDqStages][1];
+    if constexpr (QK) {
 #pragma unroll
-    for (int j = 0; j < kDqDma; ++j) issue_block(0, 0, j);
-    wait_dma();
-  }
-  __syncthreads();
+      for (int hk = 0; hk < 2; ++hk)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          s[hk][r] = 0.f;
+          dp[hk][r] = ndlt;
+        }
+    }
+    auto load_op = [&](int op) -> bf16x8 {
+      if (op < 16) {
+        const bf16* base = kprev + 2048 * (op >> 2) + 512 * (op & 3);
+        const s16x4 lo = ds_read_tr(base + tb0);
+        const s16x4 hi = ds_read_tr(base + tb1);
+        return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+      }
+      const int w = op - 16, kk = w >> 2, hk = (w >> 1) & 1;
+      return *reinterpret_cast<const bf16x8*>(((w & 1) ? vr : kr) + ((kk & 1) ? rs1 : rs0) +
+                                               4096 * hk + 256 * kk);
+    };
+    auto run_op = [&](int op, bf16x8 a) {
+      if (op < 16) {
+        dq[op & 3] = mfma32(a, zb[op >> 2], dq[op & 3]);
+      } else {
+        const int w = op - 16, kk = w >> 2, hk = (w >> 1) & 1;
+        if (w & 1) dp[hk] = mfma32(a, doreg[kk], dp[hk]);
+        else s[hk] = mfma32(a, qreg[kk], s[hk]);
+      }
+    };
+    bf16x8 queue[kDqQueue];
+#pragma unroll
+    for (int i = first; i < last + kDqQueue; ++i) {
+      if (i - kDqQueue >= first) run_op(i - kDqQueue, queue[(i - kDqQueue - first) % kDqQueue]);
+      if (i < last) queue[(i - first) % kDqQueue] = load_op(i);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
 
-  for (int t = 0; t < ntiles; ++t) {
-    const int st = t & 1;
-    // Tile t+1 into the other stage, its DMA spread over the MFMA stream.
-    const bool more = t + 1 < ntiles;
-    const bf16* kr = tiles[st][0];
-    const bf16* vr = tiles[st][1];
-    const bf16* kt = tiles[st][2];
-
-    // One unrolled stream of 48 MFMAs with a kDqQueue-deep operand queue:
-    //   ops 0-31 : kk = i / 4, half hk = (i / 2) % 2;
-    //              even: S^T[hk] += K rows x Q^T, odd: dP^T[hk] += V rows x dO^T
-    //   ops 32-47: c4 = j / 4, dt = j % 4 (j = i - 32): dQ^T[dt] += K^T x dZ^T
-    f32x16 s[2], dp[2];
+  // X block of tile t; group A first copies tile t + 2 and at the end waits
+  // for tile t + 1 (tile t + 2 may stay in flight: 8 DMA per wave per tile).
+  auto xblock = [&](int t) {
+    if (group_a && t + 2 < ntiles) issue_tile(t + 2);
+    const int kb = t * kT;
+    const bool partial = kb + kT > p.Sk;
 #pragma unroll
     for (int hk = 0; hk < 2; ++hk)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        s[hk][r] = 0.f;
-        dp[hk][r] = 0.f;
+        float pv = fast_exp2(fmaf(s[hk][r], c, -lse2));
+        if (partial && kb + 32 * hk + 8 * (r >> 2) + 4 * hh + (r & 3) >= p.Sk) pv = 0.f;
+        zb[2 * hk + (r >> 3)][r & 7] = (bf16)(pv * dp[hk][r]);
       }
-    bf16x8 zb[4];
-    auto load_op = [&](int i) -> bf16x8 {
-      if (i < 32) {
-        const int kk = i >> 2, hk = (i >> 1) & 1;
-        return *reinterpret_cast<const bf16x8*>(((i & 1) ? vr : kr) + r_rd + 4096 * hk + 256 * kk);
-      }
-      const int j = i - 32, c4 = j >> 2, dt = j & 3;
-      return *reinterpret_cast<const bf16x8*>(kt + t_rd + 2048 * dt + 256 * c4);
-    };
-    auto run_op = [&](int i, bf16x8 a) {
-      if (i < 32) {
-        const int kk = i >> 2, hk = (i >> 1) & 1;
-        if (i & 1) dp[hk] = mfma32(a, doreg[kk], dp[hk]);
-        else s[hk] = mfma32(a, qreg[kk], s[hk]);
-      } else {
-        const int j = i - 32, c4 = j >> 2, dt = j & 3;
-        dq[dt] = mfma32(a, zb[c4], dq[dt]);
-      }
-    };
-    // Register r of half hk is key kb + 32 hk + 8 (r >> 2) + 4 hh + (r & 3);
-    // keys past Sk (last tile) get P = 0.
-    const int kb = t * kT;
-    const bool partial = kb + kT > p.Sk;
-    auto form_dz = [&]() {
-#pragma unroll
-      for (int hk = 0; hk < 2; ++hk) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          float pv = fast_exp2(fmaf(s[hk][r], c, -lse2));
-          if (partial && kb + 32 * hk + 8 * (r >> 2) + 4 * hh + (r & 3) >= p.Sk) pv = 0.f;
-          zb[2 * hk + (r >> 3)][r & 7] = (bf16)(pv * (dp[hk][r] + ndlt));
-        }
-      }
-    };
-    bf16x8 queue[kDqQueue];
-    auto step = [&](int i) {  // run op i - kDqQueue, then load op i into its slot
-      const int u = i - kDqQueue;
-      if (u >= 0) run_op(u, queue[u % kDqQueue]);
-      if (i < 48) queue[i % kDqQueue] = load_op(i);
-      if (i % kDqDmaGap == 1 && i / kDqDmaGap < kDqDma && more) issue_block(t + 1, st ^ 1, i / kDqDmaGap);
-      __builtin_amdgcn_sched_barrier(0);
-    };
-#pragma unroll
-    for (int i = 0; i < 32 + kDqQueue; ++i) step(i);
-    form_dz();
-#pragma unroll
-    for (int i = 32 + kDqQueue; i < 48 + kDqQueue; ++i) step(i);
+    // The wait takes the dZ operands as inputs so that it stays after the
+    // VALU work above (a plain asm statement may be hoisted over it).
+    if (group_a) {
+      if (t + 2 < ntiles)
+        asm volatile("s_waitcnt vmcnt(8)" ::"v"(zb[0]), "v"(zb[1]), "v"(zb[2]), "v"(zb[3]) : "memory");
+      else
+        asm volatile("s_waitcnt vmcnt(0)" ::"v"(zb[0]), "v"(zb[1]), "v"(zb[2]), "v"(zb[3]) : "memory");
+    }
+  };
 
-    wait_dma();
-    __syncthreads();
+  if (ntiles > 0 && group_a) {
+    issue_tile(0);
+    if (1 < ntiles) {
+      issue_tile(1);
+      asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    } else {
+      wait_dma();
+    }
   }
+  __syncthreads();
+  if (!group_a) __syncthreads();  // the phase shift
+  if (ntiles > 0) {
+    mblock(0, std::false_type{}, std::true_type{});
+    __syncthreads();
+    xblock(0);
+    __syncthreads();
+    for (int t = 1; t < ntiles; ++t) {
+      mblock(t, std::true_type{}, std::true_type{});
+      __syncthreads();
+      xblock(t);
+      __syncthreads();
+    }
+    mblock(ntiles, std::true_type{}, std::false_type{});
+  }
+  if (group_a) __syncthreads();
 
   if (q_ok) {
     bf16* dqp = p.dq + b * p.s_dq[0] + (int64_t)qrow * p.s_dq[1] + h * p.s_dq[2] + 4 * hh;
@@ -534,15 +562,14 @@ static bool stride_ok(const int64_t* s) {
 }
 
 struct WsLayout {
-  size_t kT, stats, total;
+  size_t stats, total;
 };
 
 static WsLayout ws_layout(int64_t B, int64_t Sq, int64_t Sk, int64_t H) {
-  const int64_t ntq = (Sq + kT - 1) / kT, ntk = (Sk + kT - 1) / kT;
-  const size_t tile = (size_t)kTileElems * sizeof(bf16);
+  (void)Sk;
+  const int64_t ntq = (Sq + kT - 1) / kT;
   WsLayout w;
-  w.kT = 0;
-  w.stats = w.kT + (size_t)(B * H * ntk) * tile;
+  w.stats = 0;
   w.total = w.stats + (size_t)(B * H * ntq) * kStat * sizeof(float);
   return w;
 }
@@ -608,7 +635,6 @@ extern "C" int aa_attn_bwd(const aa_attn_bwd_args* a, void* workspace, size_t wo
     p.s_dv[i] = a->dv_stride[i];
   }
   char* ws = (char*)workspace;
-  p.kT = (bf16*)(ws + wl.kT);
   p.stats = (float*)(ws + wl.stats);
   p.H = (int)a->H;
   p.Sq = (int)a->Sq;
@@ -621,9 +647,8 @@ extern "C" int aa_attn_bwd(const aa_attn_bwd_args* a, void* workspace, size_t wo
 
   const int64_t BH = a->B * a->H;
   // Nothing reads the workspace when Sq == 0 (dK = dV = 0 and no dQ rows).
-  const int ntmax = p.ntq > p.ntk ? p.ntq : p.ntk;
   if (a->Sq > 0) {
-    bwd::prep_kernel<<<dim3((unsigned)ntmax, (unsigned)a->H, (unsigned)a->B), 256, 0, st>>>(p);
+    bwd::prep_kernel<<<dim3((unsigned)p.ntq, (unsigned)a->H, (unsigned)a->B), 256, 0, st>>>(p);
     if (int rc = check_launch("attn_bwd prep")) return rc;
   }
   if (a->Sk > 0) {

@@ -198,9 +198,8 @@ typedef struct aa_attn_bwd_args {
   int dtype;
 } aa_attn_bwd_args;
 
-/* Bytes of workspace aa_attn_bwd needs, 16-byte aligned: a transposed copy
- * of K (per 64 keys 16 KB) plus 1 KB of softmax statistics per 64 queries,
- * for every (batch, head); 0 if Sq == 0. */
+/* Bytes of workspace aa_attn_bwd needs, 16-byte aligned: 1 KB of softmax
+ * statistics per 64 queries, for every (batch, head); 0 if Sq == 0. */
 size_t aa_attn_bwd_workspace(int64_t B, int64_t Sq, int64_t Sk, int64_t H, int64_t hd);
 
 /*

@@ -89,7 +89,7 @@ def test_workspace_sizes(lib):
     assert lib.aa_attn_fwd_workspace(2, 77, 3, 128) == 2 * 3 * 2 * 16384
     assert lib.aa_attn_fwd_workspace(0, 77, 3, 128) == 0
     # 2 query tiles x (Q^T + dO^T + stats) + 2 key tiles x K^T, per (batch, head)
-    assert lib.aa_attn_bwd_workspace(2, 100, 77, 3, 128) == 2 * 3 * (2 * 1024 + 2 * 16384)
+    assert lib.aa_attn_bwd_workspace(2, 100, 77, 3, 128) == 2 * 3 * 2 * 1024
     assert lib.aa_attn_bwd_workspace(1, 0, 77, 3, 128) == 0
     assert lib.aa_qkv_norm_rope_bwd_workspace(1, 4096, 16, 128) == 256 * 2 * 128 * 4
     assert lib.aa_head_norm_bwd_workspace(2, 9, 5, 128) == 2 * 128 * 4
