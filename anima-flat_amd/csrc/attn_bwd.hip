@@ -117,14 +117,6 @@ constexpr int kDkWaves = 8;
 constexpr int kDkQueue = 8;   // A operands in flight per wave
 constexpr int kDkStages = 4;  // query tiles in the LDS ring
 
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
-
-// Transposed read: 4 bf16 per lane (tile_io.h swizzled row tile layout).
-__device__ __forceinline__ s16x4 ds_read_tr(const bf16* p) {
-  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(lds_void*)p);
-}
-
 __global__ __launch_bounds__(kDkWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void dkdv_kernel(Params p, int nkblk, int total_blocks) {
   __shared__ __attribute__((aligned(1024))) bf16 rows[kDkStages][2][kTileElems];  // [stage][Q, dO]

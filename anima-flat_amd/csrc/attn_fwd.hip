@@ -11,26 +11,26 @@
 // Transposed formulation (per wave, per 64-key tile)
 //   S^T = K Q^T   : A = K rows from the LDS row tile (32 keys x 16 d per
 //                   MFMA), B = Q^T from registers (loaded once).
-//   O^T += V^T P^T: A = V^T (32 d x 16 keys) from the LDS transposed tile,
-//                   B = P^T from the S^T accumulators.
+//   O^T += V^T P^T: A = V^T (32 d x 16 keys), read transposed from the LDS
+//                   V rows, B = P^T from the S^T accumulators.
 //   The 32x32 accumulator layout puts column j = lane%32 in every lane, with
 //   rows 8*(r/4) + 4*(lane/32) + r%4 in register r. With queries as columns,
 //   every lane holds one query: the softmax row max/sum are in-lane
 //   reductions plus one v_permlane32_swap with the partner lane, and the
 //   output rescale is a per-lane scalar multiply.
 //
-// K/V staging (tile_io.h): K rows are copied HBM -> LDS by DMA
-//   (global_load_lds_dwordx4) into the row-tile layout. V is first written
-//   to HBM in the transposed tile format by vt_pack_kernel (one pass over V,
-//   16 KB per 64 keys), then copied linearly; both operand reads are 16-byte
-//   ds_read_b128 without bank conflicts.
+// K/V staging (tile_io.h): K and V rows are copied HBM -> LDS by DMA
+//   (global_load_lds_dwordx4), K into the row-tile layout (16-byte
+//   ds_read_b128 operand reads), V into the swizzled row-tile layout, whose
+//   V^T operands are pairs of ds_read_b64_tr_b16 transposed reads. Both are
+//   free of bank conflicts.
 //
 // Key order of P^T
 //   The B operand of the MFMA wants, in lane l, 8 consecutive k-indices
 //   8*(l/32)+i of a 16-key chunk. The S^T accumulators hold, for that lane,
 //   keys {4h..4h+3, 8+4h..8+4h+3} (h = l/32) of the chunk. Since PV sums over
-//   keys, V^T only has to list its keys in the same order, which the
-//   transposed tile format does (tt_col in tile_io.h).
+//   keys, the V^T operand only has to list its keys in the same order, which
+//   the transposed reads do by addressing those rows.
 //
 // Online softmax with lazy rescaling
 //   The running max m is tracked on raw scores s = q.k; probabilities are
@@ -63,22 +63,9 @@ struct FwdParams {
   int64_t ks0, ks1, ks2;
   int64_t vs0, vs1, vs2;
   int64_t os0, os1, os2;
-  const bf16* vt;  // V repacked by vt_pack_kernel: [B][H][ntk][8192]
-  int H, Sq, Sk, nqblk, total_blocks, ntk;
+  int H, Sq, Sk, nqblk, total_blocks;
   float c;  // softmax_scale * log2(e)
 };
-
-// V^T tiles: V in the transposed tile format (columns = keys, tile_io.h),
-// one 16 KB tile per 64 keys, written by vt_pack_kernel: one workgroup per
-// (tile, head, batch); zero past Sk.
-__global__ __launch_bounds__(256) void vt_pack_kernel(const bf16* __restrict__ v, int64_t vs0,
-                                                      int64_t vs1, int64_t vs2, int Sk, int H,
-                                                      int ntk, bf16* __restrict__ vt) {
-  __shared__ __attribute__((aligned(16))) bf16 stage[kTileRows * kPackRow];
-  const int t = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-  pack_transposed_tile(v + b * vs0 + h * vs2, vs1, kTileRows * t, Sk,
-                       vt + (((int64_t)b * H + h) * ntk + t) * kTileElems, stage);
-}
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
@@ -159,23 +146,30 @@ void attn_fwd_kernel(FwdParams p) {
   const int dma_krow = 16 * (b0 >> 2) + l15;
   const int dma_chunk0 = 4 * (b0 & 3) + lq;
   const int dma_k = dma_krow * (int)p.ks1 + 8 * dma_chunk0;
-  // Rows past klen (last tile only) re-read row klen-1: finite data whose
-  // scores are masked to -inf, so their P is 0. V^T tiles come pre-packed and
-  // are copied linearly (16 KB: block b of the tile at 512 b elements).
-  const bf16* vtp = p.vt + ((int64_t)b * p.H + h) * p.ntk * 8192 + (b0 * 512 + lane * 8);
+  // V: swizzled row tile (tile_io.h), the same blocks with row slot
+  // (l & 15) ^ 4 (l >> 4). Rows past klen (last tile only) re-read row
+  // klen-1: finite data whose scores are masked to -inf, so their P is 0.
+  const int dma_vrow = 16 * (b0 >> 2) + ((lane & 15) ^ (4 * lq));
+  const int dma_v = dma_vrow * (int)p.vs1 + 8 * dma_chunk0;
   auto issue_tile = [&](int t) {
     bf16* kd = kv_lds[t % kStages][0];
     bf16* vd = kv_lds[t % kStages][1];
     const int kb = t * kBN;
-    const bf16* vsrc = vtp + (int64_t)t * 8192;
-#pragma unroll
-    for (int i = 0; i < kDmaPerWave; ++i) dma16(vsrc + 512 * i, vd + (b0 + i) * 512);
     if (kb + kBN <= klen) {
+      const bf16* vt = vp + (int64_t)kb * p.vs1 + dma_v;
+#pragma unroll
+      for (int i = 0; i < kDmaPerWave; ++i) dma16(vt + 32 * i, vd + (b0 + i) * 512);
       const bf16* kt = kp + (int64_t)kb * p.ks1 + dma_k;
 #pragma unroll
       for (int i = 0; i < kDmaPerWave; ++i) dma16(kt + 32 * i, kd + (b0 + i) * 512);
     } else {
+      const int vrow = min(kb + dma_vrow, klen - 1);
       const int krow = min(kb + dma_krow, klen - 1);
+#pragma unroll
+      for (int i = 0; i < kDmaPerWave; ++i) {
+        const int chunk = dma_chunk0 + 4 * i;
+        dma16(vp + (int64_t)vrow * p.vs1 + 8 * chunk, vd + (b0 + i) * 512);
+      }
 #pragma unroll
       for (int i = 0; i < kDmaPerWave; ++i) {
         const int chunk = dma_chunk0 + 4 * i;
@@ -185,10 +179,18 @@ void attn_fwd_kernel(FwdParams p) {
   };
 
   // Per-lane LDS read bases (elements). K operand (kt, kk): row 32kt + li,
-  // chunk 2kk + hh -> k_rd + 4096 kt + 256 kk. V^T operand (dt, c4):
-  // v_rd + 2048 dt + 256 c4.
+  // chunk 2kk + hh -> k_rd + 4096 kt + 256 kk. V^T operand (dt, c4): two
+  // ds_read_b64_tr_b16 of the swizzled V rows at v_tr[r2] + 2048 c4 + 512 dt;
+  // lane 16 G + 4 j + c addresses key 16 c4 + 4 (G >> 1) + j + 8 r2, columns
+  // 32 dt + 16 (G & 1) + 4 c .. + 3, and lane 16 G + i receives column
+  // 32 dt + 16 (G & 1) + i of those four keys: A[d][k], k = 8 (G >> 1) + 4 r2
+  // + j, the key order of the P^T B operands.
   const int k_rd = row_rd(lane);
-  const int v_rd = tt_rd(lane);
+  const int tg = lane >> 4, tj = (lane >> 2) & 3, tc = lane & 3;
+  const int v_trb = 256 * (tg & 1) + 128 * (tc >> 1) + 4 * (tc & 1) +
+                    8 * (((4 * (tg >> 1) + tj) ^ (4 * (tc >> 1))) & 7);
+  const int v_tr0 = v_trb + 64 * (tg & 1);
+  const int v_tr1 = v_trb + 64 * (1 - (tg & 1));
 
   f32x16 o[4];
 #pragma unroll
@@ -231,7 +233,10 @@ void attn_fwd_kernel(FwdParams p) {
     auto load_op = [&](int op) -> bf16x8 {
       if (op < 16) {
         const int c4 = op >> 2, dt = op & 3;
-        return *reinterpret_cast<const bf16x8*>(vs + v_rd + 2048 * dt + 256 * c4);
+        const bf16* base = vs + 2048 * c4 + 512 * dt;
+        const s16x4 lo = ds_read_tr(base + v_tr0);
+        const s16x4 hi = ds_read_tr(base + v_tr1);
+        return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
       }
       const int kk = (op - 16) >> 1, kt = (op - 16) & 1;
       return *reinterpret_cast<const bf16x8*>(ks + k_rd + 4096 * kt + 256 * kk);
@@ -379,14 +384,6 @@ static bool stride_ok(const int64_t* s) {
 
 using namespace aa;
 
-static int64_t vt_tiles(int64_t Sk) { return (Sk + kBN - 1) / kBN; }
-
-extern "C" size_t aa_attn_fwd_workspace(int64_t B, int64_t Sk, int64_t H, int64_t hd) {
-  (void)hd;
-  if (B <= 0 || Sk <= 0 || H <= 0) return 0;
-  return (size_t)(B * H * vt_tiles(Sk)) * kTileElems * sizeof(bf16);
-}
-
 // Validates args and fills the kernel parameters (no launch).
 static int prepare(const aa_attn_fwd_args* a, FwdParams& p) {
   if (!a) return fail(AA_EINVAL, "attn_fwd: null args");
@@ -409,12 +406,6 @@ static int prepare(const aa_attn_fwd_args* a, FwdParams& p) {
   // Per-lane DMA offsets within a 64-key tile are 32-bit.
   if (std::llabs(a->k_stride[1]) >= (1 << 24) || std::llabs(a->v_stride[1]) >= (1 << 24))
     return fail(AA_EUNSUPPORTED, "attn_fwd: key/value sequence stride must be < 2^24 elements");
-  const size_t ws_need = aa_attn_fwd_workspace(a->B, a->Sk, a->H, a->hd);
-  if (ws_need > 0 && (!a->workspace || a->workspace_bytes < ws_need))
-    return fail(AA_EINVAL, "attn_fwd: workspace too small");
-  if (ws_need > 0 && !aligned16(a->workspace))
-    return fail(AA_EINVAL, "attn_fwd: workspace must be 16-byte aligned");
-  if (vt_tiles(a->Sk) > 65535) return fail(AA_EUNSUPPORTED, "attn_fwd: Sk too large");
 
   p.q = (const bf16*)a->q;
   p.k = (const bf16*)a->k;
@@ -435,24 +426,7 @@ static int prepare(const aa_attn_fwd_args* a, FwdParams& p) {
   if (total > 0x7fffffff) return fail(AA_EUNSUPPORTED, "attn_fwd: grid too large");
   p.total_blocks = (int)total;
   p.c = a->softmax_scale * kLog2e;
-  p.ntk = (int)vt_tiles(a->Sk);
-  p.vt = (const bf16*)a->workspace;
   return AA_OK;
-}
-
-static int launch_pack(const aa_attn_fwd_args* a, const FwdParams& p, hipStream_t st) {
-  if (a->Sk == 0) return AA_OK;
-  vt_pack_kernel<<<dim3((unsigned)p.ntk, (unsigned)a->H, (unsigned)a->B), 256, 0, st>>>(
-      p.v, p.vs0, p.vs1, p.vs2, p.Sk, p.H, p.ntk, (bf16*)a->workspace);
-  return check_launch("attn_fwd vt_pack");
-}
-
-extern "C" int aa_attn_pack_v(const aa_attn_fwd_args* a, void* stream) {
-  clear_error();
-  FwdParams p;
-  if (int rc = prepare(a, p)) return rc;
-  if (a->B == 0 || a->Sq == 0) return AA_OK;
-  return launch_pack(a, p, (hipStream_t)stream);
 }
 
 extern "C" int aa_attn_fwd(const aa_attn_fwd_args* a, void* stream) {
@@ -461,9 +435,6 @@ extern "C" int aa_attn_fwd(const aa_attn_fwd_args* a, void* stream) {
   if (int rc = prepare(a, p)) return rc;
   if (a->B == 0 || a->Sq == 0) return AA_OK;
   hipStream_t st = (hipStream_t)stream;
-  if (!a->v_prepacked) {
-    if (int rc = launch_pack(a, p, st)) return rc;
-  }
   attn_fwd_kernel<<<dim3((unsigned)p.total_blocks), kWaves * 64, 0, st>>>(p);
   return check_launch("attn_fwd");
 }

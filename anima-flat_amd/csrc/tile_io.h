@@ -135,6 +135,16 @@ __device__ __forceinline__ void dma_row_block_swz(const bf16* base, int64_t rs, 
   dma16(base + (int64_t)row * rs + 8 * chunk, lds_tile + blk * 512);
 }
 
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// ds_read_b64_tr_b16: in each group of 16 lanes, lanes 4 j .. 4 j + 3 give
+// the addresses of the four 8-byte pieces of row j (16 consecutive bf16) and
+// lane i receives element i of rows 0..3.
+__device__ __forceinline__ s16x4 ds_read_tr(const bf16* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(lds_void*)p);
+}
+
 // DMA blocks [b0, b0 + N) of a tile stored contiguously (16 KB) at `src`.
 template <int N>
 __device__ __forceinline__ void dma_linear_tile(const bf16* src, const bf16* lds_tile, int b0,

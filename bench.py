@@ -6,15 +6,14 @@ B=1 self-attention, non-causal, q/k/v from the QK-RMSNorm + 3D-RoPE
 prologue on N(0,1) QKV), plus the per-denoiser-step attention time.
 
 A "step" is one call of the attention forward op (anima_flat::fa_fwd_nolse)
-over the config-2 batch, inputs resident in HBM; it launches two kernels,
-vt_pack_kernel (V into transposed tiles) and attn_fwd_kernel. Timing: W untimed
-steps, then K steps bracketed by torch.cuda.synchronize(); `value` =
-algorithmic FLOPs (4*B*H*Sq*Sk*d) per step / mean wall-clock step time.
-`roofline.achieved` is the same FLOPs over attn_fwd_kernel's own mean
-duration, from HIP events on the launch stream around K launches of that
-kernel alone (V packed once beforehand); the packing kernel is timed the same
-way and reported beside it. `roofline.traffic` is read from the committed
-rocprofv3 PMC summary profiles/attn_fwd_cfg2_pmc.txt.
+over the config-2 batch, inputs resident in HBM; it launches one kernel,
+attn_fwd_kernel. Timing: W untimed steps, then K steps bracketed by
+torch.cuda.synchronize(); `value` = algorithmic FLOPs (4*B*H*Sq*Sk*d) per step
+/ mean wall-clock step time. `roofline.achieved` is the same FLOPs over
+attn_fwd_kernel's own mean duration, from HIP events on the launch stream
+around K launches made straight through the C ABI (no torch allocation in
+between). `roofline.traffic` is read from the committed rocprofv3 PMC summary
+profiles/attn_fwd_cfg2_pmc.txt.
 
 Extra fields report the other kernels of the path: prologue and head_norm
 HBM GB/s, masked cross-attention (config 3), forward+backward (config 5),
@@ -85,27 +84,19 @@ def prewarm(fn, seconds: float = 0.5) -> None:
 
 
 def kernel_only_timer(pkg, q, k, v):
-    """Launchers for the two kernels of one forward (V packing, attention with the
-    V already packed), called straight through the C ABI on torch's current stream."""
+    """Launcher of attn_fwd_kernel alone: aa_attn_fwd called straight through the
+    C ABI on torch's current stream, into a preallocated output."""
     A = sys.modules[pkg.__name__ + ".attention"]
     L = pkg._lib
     out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
     args = A._fwd_args(q, k, v, out, None, None, None)
-    nbytes = L.lib().aa_attn_fwd_workspace(q.shape[0], k.shape[1], q.shape[2], q.shape[3])
-    ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
-    args.workspace, args.workspace_bytes = ws.data_ptr(), nbytes
     stream = L.stream(q)
-    L.check(L.lib().aa_attn_pack_v(ctypes.byref(args), stream), "attn_pack_v")
-    packed = L.AttnFwdArgs.from_buffer_copy(args)
-    packed.v_prepacked = 1
-
-    def pack():
-        L.lib().aa_attn_pack_v(ctypes.byref(args), stream)
+    L.check(L.lib().aa_attn_fwd(ctypes.byref(args), stream), "attn_fwd")
 
     def attn():
-        L.lib().aa_attn_fwd(ctypes.byref(packed), stream)
+        L.lib().aa_attn_fwd(ctypes.byref(args), stream)
 
-    return pack, attn, (out, ws)
+    return attn, out
 
 
 def pmc_traffic(name: str):
@@ -191,12 +182,10 @@ def main() -> int:
     p = prologue_qkv(pkg, B, S, H, 1002, dev)
     with torch.no_grad():
         q, k, v = pkg.qkv_norm_rope(p["qkv"], p["q_weight"], p["k_weight"], p["cos"], p["sin"], H, eps)
-        # The dominant kernel alone (attention with V already packed) and the
-        # packing pass (vt_pack_kernel) on its own.
-        pack, attn, keep = kernel_only_timer(pkg, q, k, v)
+        # The kernel alone, launched through the C ABI.
+        attn, keep = kernel_only_timer(pkg, q, k, v)
         prewarm(attn)
         _, attn_ms = time_launches(attn, args.steps, args.warmup)
-        _, pack_ms = time_launches(pack, max(10, args.steps // 2), 3)
         fwd = torch.ops.anima_flat.fa_fwd_nolse
         wall_ms, dev_ms = time_launches(lambda: fwd(q, k, v), args.steps, args.warmup)
     if args.copy_calibration:
@@ -241,8 +230,6 @@ def main() -> int:
             "traffic": pmc_traffic("attn_fwd_cfg2_pmc.txt"),
             "kernel": "attn_fwd_kernel",
             "kernel_us": round(attn_ms * 1e3, 2),
-            "pack_kernel": "vt_pack_kernel",
-            "pack_kernel_us": round(pack_ms * 1e3, 2),
         },
     }
 

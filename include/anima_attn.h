@@ -143,20 +143,13 @@ typedef struct aa_attn_fwd_args {
   int64_t B, Sq, Sk, H, hd;
   float softmax_scale;  /* usually 1/sqrt(hd) */
   int dtype;
-  void* workspace;      /* device scratch of aa_attn_fwd_workspace() bytes */
-  size_t workspace_bytes;
-  int v_prepacked;      /* nonzero: workspace already holds v packed by
-                           aa_attn_pack_v (the packing pass is skipped) */
 } aa_attn_fwd_args;
-
-/* Bytes of device workspace aa_attn_fwd needs: V repacked as transposed
- * 64-key tiles (B * H * ceil(Sk / 64) * 16 KiB). */
-size_t aa_attn_fwd_workspace(int64_t B, int64_t Sk, int64_t H, int64_t hd);
 
 /*
  * out = softmax(q k^T * softmax_scale) v, non-causal, per (batch, head);
  * keys j >= seqused_k[b] are excluded when seqused_k != NULL; lse is the
  * natural-log row log-sum-exp of the scaled scores over the attended keys.
+ * One kernel launch, no device workspace.
  * Replaces: src/attention.py:43-53 (anima_flat::fa_fwd),
  *           src/attention.py:63-66 (anima_flat::fa_fwd_nolse),
  *           src/attention.py:74-81 (anima_flat::fa_fwd_k), and with
@@ -164,16 +157,6 @@ size_t aa_attn_fwd_workspace(int64_t B, int64_t Sk, int64_t H, int64_t hd);
  *           src/attention.py:156-180 (cross_attention_trimmed).
  */
 int aa_attn_fwd(const aa_attn_fwd_args* args, void* stream);
-
-/*
- * Packs args->v into args->workspace (transposed 64-key tiles) exactly as
- * aa_attn_fwd does before its main kernel; a later aa_attn_fwd with
- * v_prepacked = 1 and the same v, Sk, B, H reuses it (e.g. cross-attention
- * keys/values that stay fixed across denoising steps).
- * Replaces: no separate reference function (part of the FA4 call at
- *           src/attention.py:63-66).
- */
-int aa_attn_pack_v(const aa_attn_fwd_args* args, void* stream);
 
 typedef struct aa_attn_bwd_args {
   const void* dout;     /* [B, Sq, H, hd] */

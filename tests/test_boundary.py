@@ -46,7 +46,6 @@ def test_header_declares_the_entry_points():
         "aa_head_norm_fwd",
         "aa_head_norm_bwd",
         "aa_attn_fwd",
-        "aa_attn_fwd_workspace",
         "aa_attn_bwd",
         "aa_attn_bwd_workspace",
         "aa_ctx_scale_fwd",
@@ -85,10 +84,7 @@ def test_structs_match_header_field_order(pkg):
 
 
 def test_workspace_sizes(lib):
-    assert lib.aa_attn_fwd_workspace(1, 4096, 16, 128) == 16 * 64 * 16384
-    assert lib.aa_attn_fwd_workspace(2, 77, 3, 128) == 2 * 3 * 2 * 16384
-    assert lib.aa_attn_fwd_workspace(0, 77, 3, 128) == 0
-    # 2 query tiles x (Q^T + dO^T + stats) + 2 key tiles x K^T, per (batch, head)
+    # one 1 KB stats record per 64-query tile, per (batch, head)
     assert lib.aa_attn_bwd_workspace(2, 100, 77, 3, 128) == 2 * 3 * 2 * 1024
     assert lib.aa_attn_bwd_workspace(1, 0, 77, 3, 128) == 0
     assert lib.aa_qkv_norm_rope_bwd_workspace(1, 4096, 16, 128) == 256 * 2 * 128 * 4
