@@ -17,7 +17,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().with_name("libanima_attn.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 AA_OK = 0
 AA_EINVAL = -1

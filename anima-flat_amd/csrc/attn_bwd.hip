@@ -169,21 +169,11 @@ void dkdv_kernel(Params p, int nkblk, int total_blocks) {
     if (wave == 4) dma16(statb + (int64_t)t * kStat + 4 * lane, stat[st]);
   };
 
-  // Per-lane read offsets (elements) in a swizzled row tile.
-  // Row operand of op (hq, kk) = row 32 hq + li, chunk 2 kk + hh: slot
-  // (li & 15) ^ 4 (2 (kk & 1) + hh); base rs[kk & 1], + 4096 hq + 256 kk.
-  const int rs0 = (li >> 4) * 2048 + hh * 128 + (((li & 15) ^ (4 * hh)) * 8);
-  const int rs1 = (li >> 4) * 2048 + hh * 128 + (((li & 15) ^ (8 + 4 * hh)) * 8);
-  // Transposed operand of op (c4, dt), lane 16 G + 4 j + c: two reads r2 =
-  // 0, 1 of rows (queries) 16 c4 + 4 (G >> 1) + j + 8 r2, columns 32 dt +
-  // 16 (G & 1) + 4 c .. + 3; lane 16 G + i receives column 32 dt + 16 (G & 1)
-  // + i of those four rows, i.e. A[d][k] with k = 8 (G >> 1) + 4 r2 + j, the
-  // query order of the P / dZ B operands. Base tb[r2], + 2048 c4 + 512 dt.
-  const int G = lane >> 4, tj = (lane >> 2) & 3, tc = lane & 3;
-  const int tbase = 256 * (G & 1) + 128 * (tc >> 1) + 4 * (tc & 1) +
-                    8 * (((4 * (G >> 1) + tj) ^ (4 * (tc >> 1))) & 7);
-  const int tb0 = tbase + 64 * (G & 1);
-  const int tb1 = tbase + 64 * (1 - (G & 1));
+  // Per-lane read offsets in the swizzled row tiles (tile_io.h): row operand
+  // (hq, kk) at rs[kk & 1] + 4096 hq + 256 kk; transposed operand (c4, dt),
+  // queries in the order of the P / dZ B operands, via tb0 / tb1.
+  const int rs0 = swz_row_rd(lane, 0), rs1 = swz_row_rd(lane, 1);
+  const int tb0 = swz_tr_rd(lane, 0), tb1 = swz_tr_rd(lane, 1);
   const float c = p.c;
 
   f32x16 acc[4];  // dV^T (A) or dK^T (B)
@@ -220,12 +210,7 @@ void dkdv_kernel(Params p, int nkblk, int total_blocks) {
         }
     }
     auto load_op = [&](int op) -> bf16x8 {
-      if (op < 16) {
-        const bf16* base = tt + 2048 * (op >> 2) + 512 * (op & 3);
-        const s16x4 lo = ds_read_tr(base + tb0);
-        const s16x4 hi = ds_read_tr(base + tb1);
-        return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-      }
+      if (op < 16) return read_tr_operand(tt, op >> 2, op & 3, tb0, tb1);
       const int w = op - 16;
       return *reinterpret_cast<const bf16x8*>(rr + ((w & 1) ? rs1 : rs0) + 4096 * (w >> 3) +
                                                256 * (w & 7));
@@ -410,16 +395,11 @@ void dq_kernel(Params p, int nqblk, int total_blocks) {
       dma_row_block_swz(vbase + (int64_t)k0 * p.s_v[1], p.s_v[1], nr, tiles[st][1], g4 + i, lane);
   };
 
-  // Read offsets in the swizzled row tiles, as in dkdv_kernel: row operands
-  // (row 32 hk + li, chunk 2 kk + hh) at rs[kk & 1] + 4096 hk + 256 kk;
-  // transposed operands (c4, dt) at tb[r2] + 2048 c4 + 512 dt.
-  const int rs0 = (li >> 4) * 2048 + hh * 128 + (((li & 15) ^ (4 * hh)) * 8);
-  const int rs1 = (li >> 4) * 2048 + hh * 128 + (((li & 15) ^ (8 + 4 * hh)) * 8);
-  const int G = lane >> 4, tj = (lane >> 2) & 3, tc = lane & 3;
-  const int tbase = 256 * (G & 1) + 128 * (tc >> 1) + 4 * (tc & 1) +
-                    8 * (((4 * (G >> 1) + tj) ^ (4 * (tc >> 1))) & 7);
-  const int tb0 = tbase + 64 * (G & 1);
-  const int tb1 = tbase + 64 * (1 - (G & 1));
+  // Read offsets in the swizzled row tiles (tile_io.h): row operands (row
+  // 32 hk + li, chunk 2 kk + hh) at rs[kk & 1] + 4096 hk + 256 kk; transposed
+  // operands (c4, dt), keys in the order of the dZ^T B operands, via tb0 / tb1.
+  const int rs0 = swz_row_rd(lane, 0), rs1 = swz_row_rd(lane, 1);
+  const int tb0 = swz_tr_rd(lane, 0), tb1 = swz_tr_rd(lane, 1);
   const float c = p.c;
 
   f32x16 dq[4];
@@ -455,12 +435,7 @@ void dq_kernel(Params p, int nqblk, int total_blocks) {
         }
     }
     auto load_op = [&](int op) -> bf16x8 {
-      if (op < 16) {
-        const bf16* base = kprev + 2048 * (op >> 2) + 512 * (op & 3);
-        const s16x4 lo = ds_read_tr(base + tb0);
-        const s16x4 hi = ds_read_tr(base + tb1);
-        return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-      }
+      if (op < 16) return read_tr_operand(kprev, op >> 2, op & 3, tb0, tb1);
       const int w = op - 16, kk = w >> 2, hk = (w >> 1) & 1;
       return *reinterpret_cast<const bf16x8*>(((w & 1) ? vr : kr) + ((kk & 1) ? rs1 : rs0) +
                                                4096 * hk + 256 * kk);

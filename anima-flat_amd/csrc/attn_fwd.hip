@@ -146,9 +146,9 @@ void attn_fwd_kernel(FwdParams p) {
   const int dma_krow = 16 * (b0 >> 2) + l15;
   const int dma_chunk0 = 4 * (b0 & 3) + lq;
   const int dma_k = dma_krow * (int)p.ks1 + 8 * dma_chunk0;
-  // V: swizzled row tile (tile_io.h), the same blocks with row slot
-  // (l & 15) ^ 4 (l >> 4). Rows past klen (last tile only) re-read row
-  // klen-1: finite data whose scores are masked to -inf, so their P is 0.
+  // V: swizzled row tile (tile_io.h, dma_row_block_swz), the same blocks with
+  // row slot (l & 15) ^ 4 (l >> 4). Rows past klen (last tile only) re-read
+  // row klen-1: finite data whose scores are masked to -inf, so their P is 0.
   const int dma_vrow = 16 * (b0 >> 2) + ((lane & 15) ^ (4 * lq));
   const int dma_v = dma_vrow * (int)p.vs1 + 8 * dma_chunk0;
   auto issue_tile = [&](int t) {
@@ -178,19 +178,12 @@ void attn_fwd_kernel(FwdParams p) {
     }
   };
 
-  // Per-lane LDS read bases (elements). K operand (kt, kk): row 32kt + li,
-  // chunk 2kk + hh -> k_rd + 4096 kt + 256 kk. V^T operand (dt, c4): two
-  // ds_read_b64_tr_b16 of the swizzled V rows at v_tr[r2] + 2048 c4 + 512 dt;
-  // lane 16 G + 4 j + c addresses key 16 c4 + 4 (G >> 1) + j + 8 r2, columns
-  // 32 dt + 16 (G & 1) + 4 c .. + 3, and lane 16 G + i receives column
-  // 32 dt + 16 (G & 1) + i of those four keys: A[d][k], k = 8 (G >> 1) + 4 r2
-  // + j, the key order of the P^T B operands.
+  // Per-lane LDS read offsets (elements). K operand (kt, kk): row 32kt + li,
+  // chunk 2kk + hh -> k_rd + 4096 kt + 256 kk. V^T operand (dt, c4): the
+  // transposed read of the swizzled V rows (tile_io.h), keys in the order of
+  // the P^T B operands.
   const int k_rd = row_rd(lane);
-  const int tg = lane >> 4, tj = (lane >> 2) & 3, tc = lane & 3;
-  const int v_trb = 256 * (tg & 1) + 128 * (tc >> 1) + 4 * (tc & 1) +
-                    8 * (((4 * (tg >> 1) + tj) ^ (4 * (tc >> 1))) & 7);
-  const int v_tr0 = v_trb + 64 * (tg & 1);
-  const int v_tr1 = v_trb + 64 * (1 - (tg & 1));
+  const int v_tr0 = swz_tr_rd(lane, 0), v_tr1 = swz_tr_rd(lane, 1);
 
   f32x16 o[4];
 #pragma unroll
@@ -231,13 +224,7 @@ void attn_fwd_kernel(FwdParams p) {
     }
     bf16x8 q_ops[kPrefetch];
     auto load_op = [&](int op) -> bf16x8 {
-      if (op < 16) {
-        const int c4 = op >> 2, dt = op & 3;
-        const bf16* base = vs + 2048 * c4 + 512 * dt;
-        const s16x4 lo = ds_read_tr(base + v_tr0);
-        const s16x4 hi = ds_read_tr(base + v_tr1);
-        return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-      }
+      if (op < 16) return read_tr_operand(vs, op >> 2, op & 3, v_tr0, v_tr1);
       const int kk = (op - 16) >> 1, kt = (op - 16) & 1;
       return *reinterpret_cast<const bf16x8*>(ks + k_rd + 4096 * kt + 256 * kk);
     };

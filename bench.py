@@ -280,6 +280,7 @@ def main() -> int:
             out = pkg.attention(qg, kg, vg)
             torch.autograd.grad(out, (qg, kg, vg), dout)
 
+        prewarm(fwd_bwd, 0.3)
         _, us_fb = time_launches(fwd_bwd, max(5, steps // 2), 2)
         fb_flops = 3.5 * flops
         extras["fwd_bwd_cfg5"] = {

@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define AA_ABI_VERSION 1
+#define AA_ABI_VERSION 2
 
 enum {
   AA_OK = 0,
