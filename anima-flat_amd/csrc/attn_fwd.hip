@@ -85,136 +85,126 @@ constexpr int kDmaWaves = 4; // group A issues every DMA
 constexpr int kStages = 4;   // K/V ring depth (4 x 32 KB)
 constexpr int kAhead = kStages - 2;  // tiles of DMA in flight beyond the next one
 constexpr int kQPerWg = kWaves * 32;
+constexpr int kDmaPerWave = 16 / kDmaWaves;  // 1 KB DMA blocks per group-A wave per tile, K and V each
+static_assert(2 * kDmaPerWave == 8, "the DMA waits count 8 instructions per tile");
 
-// Phase-shifted ("ping-pong") schedule. Waves 0-3 (group A) and 4-7 (group B)
-// run the same per-tile work, one phase apart:
-//   M(j): O^T += V_{j-1}^T P_{j-1}^T (16 MFMA) and S_j^T = K_j Q^T (16 MFMA)
-//   X(j): softmax of S_j -> P_j (exp, max, sums, rare rescale)
-//   phase 2j  : A runs M(j), B runs X(j-1)
-//   phase 2j+1: A runs X(j), B runs M(j)
-// with a workgroup barrier between phases. Waves w and w+4 share a SIMD, so
-// on every SIMD one wave is in an MFMA block while its partner is in a VALU
-// block and the matrix and vector pipes overlap. Tile j sits in stage
-// j % kStages; its DMA is issued at phase 2(j-kAhead)+1 and complete (wait +
-// barrier) by the end of phase 2j-1; its K is read in phases 2j, 2j+1 and
-// its V in 2j+2, 2j+3.
-__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void attn_fwd_kernel(FwdParams p) {
-  constexpr int kDmaPerWave = 16 / kDmaWaves;  // 1 KB DMA blocks per group-A wave per tile, K and V each
-  __shared__ __attribute__((aligned(1024))) bf16 kv_lds[kStages][2][kTileElems];
+// (batch, head, query block) of one work item; klen keys attended.
+struct Item {
+  int b, h, qblk, klen, ntiles;
+};
 
-  // Block -> (batch, head, query block), XCD-aware: the query blocks of one
-  // head share an XCD and its L2.
-  const int logical = xcd_remap(blockIdx.x, p.total_blocks);
-  const int qblk = logical % p.nqblk;
-  const int bh = logical / p.nqblk;
-  const int b = bh / p.H;
-  const int h = bh - b * p.H;
+__device__ __forceinline__ Item decode_item(const FwdParams& p, int it) {
+  Item r;
+  r.qblk = it % p.nqblk;
+  const int bh = it / p.nqblk;
+  r.b = bh / p.H;
+  r.h = bh - r.b * p.H;
+  r.klen = p.seqused ? min((int)p.seqused[r.b], p.Sk) : p.Sk;
+  r.ntiles = r.klen > 0 ? (r.klen + kBN - 1) / kBN : 0;
+  return r;
+}
 
-  const int tid = threadIdx.x;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const bool group_a = wave < 4;
-  const int lane = tid & 63;
-  const int li = lane & 31;
-  const int hh = lane >> 5;
+// K/V tile DMA of one group-A wave: K into the row tile, V into the swizzled
+// row tile (tile_io.h). A DMA instruction fills 1 KB = one 16-row group x 4
+// chunks; wave w fills blocks 4 w .. 4 w + 3, i.e. rows 16 w .. 16 w + 15 in
+// chunks lq + 4 i. Rows past klen (last tile only) re-read row klen-1: finite
+// data whose scores are masked to -inf, so their P is 0.
+struct KVDma {
+  int b0, krow, vrow, chunk0, koff, voff;
 
-  const int klen = p.seqused ? min((int)p.seqused[b], p.Sk) : p.Sk;
-  const int ntiles = klen > 0 ? (klen + kBN - 1) / kBN : 0;
+  __device__ __forceinline__ void setup(const FwdParams& p, int wave, int lane) {
+    b0 = wave * kDmaPerWave;
+    const int lq = lane >> 4;
+    krow = 16 * (b0 >> 2) + (lane & 15);
+    vrow = 16 * (b0 >> 2) + ((lane & 15) ^ (4 * lq));
+    chunk0 = 4 * (b0 & 3) + lq;
+    koff = krow * (int)p.ks1 + 8 * chunk0;
+    voff = vrow * (int)p.vs1 + 8 * chunk0;
+  }
 
-  // Q^T operand: lane holds Q[query li][16*kk + 8*hh + 0..7] for kk = 0..7.
-  const int qrow = qblk * kQPerWg + wave * 32 + li;
-  bf16x8 qreg[8];
-  {
-    const bf16* qp = p.q + b * p.qs0 + h * p.qs2 + (int64_t)qrow * p.qs1 + 8 * hh;
+  // Tile t (keys 64 t ..) of the (batch, head) at kp / vp into kd / vd.
+  __device__ __forceinline__ void issue(const FwdParams& p, const bf16* kp, const bf16* vp, int klen,
+                                        int t, bf16* kd, bf16* vd) const {
+    const int kb = t * kBN;
+    if (kb + kBN <= klen) {
+      const bf16* vt = vp + (int64_t)kb * p.vs1 + voff;
+#pragma unroll
+      for (int i = 0; i < kDmaPerWave; ++i) dma16(vt + 32 * i, vd + (b0 + i) * 512);
+      const bf16* kt = kp + (int64_t)kb * p.ks1 + koff;
+#pragma unroll
+      for (int i = 0; i < kDmaPerWave; ++i) dma16(kt + 32 * i, kd + (b0 + i) * 512);
+    } else {
+      const int vr = min(kb + vrow, klen - 1);
+      const int kr = min(kb + krow, klen - 1);
+#pragma unroll
+      for (int i = 0; i < kDmaPerWave; ++i)
+        dma16(vp + (int64_t)vr * p.vs1 + 8 * (chunk0 + 4 * i), vd + (b0 + i) * 512);
+#pragma unroll
+      for (int i = 0; i < kDmaPerWave; ++i)
+        dma16(kp + (int64_t)kr * p.ks1 + 8 * (chunk0 + 4 * i), kd + (b0 + i) * 512);
+    }
+  }
+};
+
+// Per-wave state and work of the forward: 32 queries, their Q^T operands,
+// O^T accumulators and running softmax statistics.
+struct FwdWave {
+  bf16x8 qreg[8];  // Q^T operand: lane holds Q[query li][16 kk + 8 hh + 0..7]
+  f32x16 o[4];     // O^T, d = 32 dt + rows
+  // Running max in raw score units (before the scale); l partial sums in
+  // four independent chains.
+  float m_raw;
+  float l4[4];
+  f32x16 s0, s1;  // S^T of the tile between its M and X blocks
+  bf16x8 pb[4];   // P^T of the tile between its X block and the next M block
+  int hh, li, k_rd, v_tr0, v_tr1;
+  float c, thr_raw;
+
+  __device__ __forceinline__ void setup(int lane, float c_) {
+    li = lane & 31;
+    hh = lane >> 5;
+    // K operand (kt, kk): row 32 kt + li, chunk 2 kk + hh -> k_rd + 4096 kt
+    // + 256 kk. V^T operand (dt, c4): the transposed read of the swizzled V
+    // rows (tile_io.h), keys in the order of the P^T B operands.
+    k_rd = row_rd(lane);
+    v_tr0 = swz_tr_rd(lane, 0);
+    v_tr1 = swz_tr_rd(lane, 1);
+    c = c_;
+    thr_raw = kRescaleThreshold / c;
+  }
+
+  __device__ __forceinline__ void reset() {
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[dt][r] = 0.f;
+    m_raw = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) l4[i] = 0.f;
+  }
+
+  __device__ __forceinline__ void load_q(const FwdParams& p, const Item& it, int qrow,
+                                         bf16x8 (&dst)[8]) const {
+    const bf16* qp = p.q + it.b * p.qs0 + it.h * p.qs2 + (int64_t)qrow * p.qs1 + 8 * hh;
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk) {
       u32x4 w = {0u, 0u, 0u, 0u};
       if (qrow < p.Sq) w = ld16(qp + 16 * kk);
-      qreg[kk] = as_bf16x8(w);
+      dst[kk] = as_bf16x8(w);
     }
   }
 
-  const bf16* kp = p.k + b * p.ks0 + h * p.ks2;
-  const bf16* vp = p.v + b * p.vs0 + h * p.vs2;
-
-  // K: row tile (tile_io.h). A DMA instruction fills 1 KB = one 16-row group
-  // x 4 chunks; lane l writes slot l & 15 of chunk 4 (blk & 3) + (l >> 4), so
-  // it fetches row 16 (blk >> 2) + (l & 15). For a full tile the offsets are
-  // one per-lane base plus 32 elements per further block of the same wave.
-  const int b0 = wave * kDmaPerWave;
-  const int l15 = lane & 15, lq = lane >> 4;
-  const int dma_krow = 16 * (b0 >> 2) + l15;
-  const int dma_chunk0 = 4 * (b0 & 3) + lq;
-  const int dma_k = dma_krow * (int)p.ks1 + 8 * dma_chunk0;
-  // V: swizzled row tile (tile_io.h, dma_row_block_swz), the same blocks with
-  // row slot (l & 15) ^ 4 (l >> 4). Rows past klen (last tile only) re-read
-  // row klen-1: finite data whose scores are masked to -inf, so their P is 0.
-  const int dma_vrow = 16 * (b0 >> 2) + ((lane & 15) ^ (4 * lq));
-  const int dma_v = dma_vrow * (int)p.vs1 + 8 * dma_chunk0;
-  auto issue_tile = [&](int t) {
-    bf16* kd = kv_lds[t % kStages][0];
-    bf16* vd = kv_lds[t % kStages][1];
-    const int kb = t * kBN;
-    if (kb + kBN <= klen) {
-      const bf16* vt = vp + (int64_t)kb * p.vs1 + dma_v;
-#pragma unroll
-      for (int i = 0; i < kDmaPerWave; ++i) dma16(vt + 32 * i, vd + (b0 + i) * 512);
-      const bf16* kt = kp + (int64_t)kb * p.ks1 + dma_k;
-#pragma unroll
-      for (int i = 0; i < kDmaPerWave; ++i) dma16(kt + 32 * i, kd + (b0 + i) * 512);
-    } else {
-      const int vrow = min(kb + dma_vrow, klen - 1);
-      const int krow = min(kb + dma_krow, klen - 1);
-#pragma unroll
-      for (int i = 0; i < kDmaPerWave; ++i) {
-        const int chunk = dma_chunk0 + 4 * i;
-        dma16(vp + (int64_t)vrow * p.vs1 + 8 * chunk, vd + (b0 + i) * 512);
-      }
-#pragma unroll
-      for (int i = 0; i < kDmaPerWave; ++i) {
-        const int chunk = dma_chunk0 + 4 * i;
-        dma16(kp + (int64_t)krow * p.ks1 + 8 * chunk, kd + (b0 + i) * 512);
-      }
-    }
-  };
-
-  // Per-lane LDS read offsets (elements). K operand (kt, kk): row 32kt + li,
-  // chunk 2kk + hh -> k_rd + 4096 kt + 256 kk. V^T operand (dt, c4): the
-  // transposed read of the swizzled V rows (tile_io.h), keys in the order of
-  // the P^T B operands.
-  const int k_rd = row_rd(lane);
-  const int v_tr0 = swz_tr_rd(lane, 0), v_tr1 = swz_tr_rd(lane, 1);
-
-  f32x16 o[4];
-#pragma unroll
-  for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) o[dt][r] = 0.f;
-  // Running max in raw score units (before the scale); l partial sums in
-  // four independent chains.
-  float m_raw = -INFINITY;
-  float l4[4] = {0.f, 0.f, 0.f, 0.f};
-  const float c = p.c;
-  const float thr_raw = kRescaleThreshold / c;
-  const bf16x2 ones = {(bf16)1.0f, (bf16)1.0f};
-  f32x16 s0, s1;  // S^T of the tile between its M and X blocks
-  bf16x8 pb[4];   // P^T of the tile between its X block and the next M block
-
   // M block: up to 32 MFMAs in one unrolled stream, fed by a queue of LDS
   // operands read kPrefetch MFMAs ahead (sched_barrier fences pin the order):
-  //   ops 0-15 : O^T += V^T P^T of tile tv, op = 4 c4 + dt (A operand: one
-  //              16-byte read of the V^T tile)
-  //   ops 16-31: S^T = K Q^T of tile tk, op = 16 + 2 kk + kt (A operand: one
-  //              16-byte read of the K tile; two accumulator chains s0, s1)
+  //   ops 0-15 : O^T += V^T P^T of the V tile vs, op = 4 c4 + dt (A operand:
+  //              the transposed read of the V rows)
+  //   ops 16-31: S^T = K Q^T of the K tile ks, op = 16 + 2 kk + kt (A operand:
+  //              one 16-byte read of the K tile; two accumulator chains s0, s1)
   // PV / QK select which half runs (the first tile has no PV, the tail no QK).
-  constexpr int kPrefetch = 12;
-  auto mblock = [&](int tv, int tk, auto pv_tag, auto qk_tag) {
-    constexpr bool PV = decltype(pv_tag)::value;
-    constexpr bool QK = decltype(qk_tag)::value;
+  template <bool PV, bool QK, int kPrefetch = 12>
+  __device__ __forceinline__ void mblock(const bf16* vs, const bf16* ks) {
     constexpr int first = PV ? 0 : 16;
     constexpr int last = QK ? 32 : 16;
-    const bf16* vs = kv_lds[tv % kStages][1];
-    const bf16* ks = kv_lds[tk % kStages][0];
     if constexpr (QK) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
@@ -245,10 +235,12 @@ void attn_fwd_kernel(FwdParams p) {
       if (i < last) q_ops[(i - first) % kPrefetch] = load_op(i);
       __builtin_amdgcn_sched_barrier(0);
     }
-  };
-  // Softmax of tile t: mask (last tile only), row max, lazy rescale, P, sums.
-  auto softmax = [&](int t) {
-    const int kb = t * kBN;
+  }
+
+  // Softmax of the tile at key offset kb: mask (last tile only), row max,
+  // lazy rescale, P, sums.
+  __device__ __forceinline__ void softmax(int kb, int klen) {
+    const bf16x2 ones = {(bf16)1.0f, (bf16)1.0f};
     if (kb + kBN > klen) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
@@ -299,16 +291,79 @@ void attn_fwd_kernel(FwdParams p) {
         l4[c4] = __builtin_amdgcn_fdot2_f32_bf16(pair, ones, l4[c4], false);
       }
     }
+  }
+
+  // Normalise, optional padding correction, store O and LSE of query qrow.
+  __device__ __forceinline__ void epilogue(const FwdParams& p, const Item& it, int qrow) const {
+    const float m_run = m_raw * c;
+    const float l_run = (l4[0] + l4[1]) + (l4[2] + l4[3]);
+    const float l_tot = pair_sum(l_run);
+    const bool any = l_tot > 0.f;
+    const float lse = any ? (m_run + __log2f(l_tot)) * kLn2 : -INFINITY;
+    float scale = any ? 1.0f / l_tot : 0.f;
+    if (p.ln_pad) scale *= 1.0f / (1.0f + expf(p.ln_pad[it.b] - lse));
+    if (qrow < p.Sq) {
+      bf16* op = p.o + it.b * p.os0 + (int64_t)qrow * p.os1 + it.h * p.os2 + 4 * hh;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+#pragma unroll
+        for (int rq = 0; rq < 4; ++rq) {
+          u32x2 w = {pack_bf16(o[dt][4 * rq] * scale, o[dt][4 * rq + 1] * scale),
+                     pack_bf16(o[dt][4 * rq + 2] * scale, o[dt][4 * rq + 3] * scale)};
+          *reinterpret_cast<u32x2*>(op + 32 * dt + 8 * rq) = w;
+        }
+      }
+      if (p.lse && hh == 0) p.lse[((int64_t)it.b * p.H + it.h) * p.Sq + qrow] = lse;
+    }
+  }
+};
+
+// Phase-shifted ("ping-pong") schedule. Waves 0-3 (group A) and 4-7 (group B)
+// run the same per-tile work, one phase apart:
+//   M(j): O^T += V_{j-1}^T P_{j-1}^T (16 MFMA) and S_j^T = K_j Q^T (16 MFMA)
+//   X(j): softmax of S_j -> P_j (exp, max, sums, rare rescale)
+//   phase 2j  : A runs M(j), B runs X(j-1)
+//   phase 2j+1: A runs X(j), B runs M(j)
+// with a workgroup barrier between phases. Waves w and w+4 share a SIMD, so
+// on every SIMD one wave is in an MFMA block while its partner is in a VALU
+// block and the matrix and vector pipes overlap. Tile j sits in stage
+// j % kStages; its DMA is issued at phase 2(j-kAhead)+1 and complete (wait +
+// barrier) by the end of phase 2j-1; its K is read in phases 2j, 2j+1 and
+// its V in 2j+2, 2j+3. Both groups run the same instruction stream,
+// M(m) | barrier | X(m) | barrier; group B executes one extra barrier first
+// (group A one extra at the end), which shifts B by exactly one phase. Only
+// group A issues and waits for the DMA: tile m+kAhead at the start of its
+// X(m), off the MFMA stream (the stage it overwrites held tile m-2, whose V
+// group B last read in phase 2m-1), and tile m+1 is complete before the
+// barrier that ends its X(m); the barriers order it for group B.
+//
+// One workgroup per work item (256 queries of one (batch, head)).
+__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void attn_fwd_kernel(FwdParams p) {
+  __shared__ __attribute__((aligned(1024))) bf16 kv_lds[kStages][2][kTileElems];
+
+  // Block -> work item, XCD-aware: the query blocks of one head share an XCD
+  // and its L2.
+  const Item it = decode_item(p, xcd_remap(blockIdx.x, p.total_blocks));
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool group_a = wave < 4;
+  const int lane = tid & 63;
+  const int qrow = it.qblk * kQPerWg + wave * 32 + (lane & 31);
+  const int ntiles = it.ntiles;
+
+  FwdWave w;
+  w.setup(lane, p.c);
+  w.load_q(p, it, qrow, w.qreg);
+  w.reset();
+  KVDma dma;
+  dma.setup(p, wave, lane);
+  const bf16* kp = p.k + it.b * p.ks0 + it.h * p.ks2;
+  const bf16* vp = p.v + it.b * p.vs0 + it.h * p.vs2;
+  auto issue_tile = [&](int t) {
+    dma.issue(p, kp, vp, it.klen, t, kv_lds[t % kStages][0], kv_lds[t % kStages][1]);
   };
 
-  // Both groups run the same instruction stream, M(m) | barrier | X(m) |
-  // barrier; group B executes one extra barrier first (group A one extra at
-  // the end), which shifts B by exactly one phase. Only group A issues and
-  // waits for the DMA: tile m+kAhead at the start of its X(m), off the MFMA
-  // stream (the stage it overwrites held tile m+kAhead-kStages = m-2, whose V
-  // group B last read in phase 2m-1), and tile m+1 is complete before the
-  // barrier that ends its X(m); the barriers order it for group B.
-  static_assert(2 * kDmaPerWave == 8, "wait_dma_tiles_in_flight counts 8 DMA per tile");
   static_assert(kAhead >= 1 && kAhead <= 4, "lookahead");
   auto wait_for_next = [&](int m) {  // tile m+1 complete; later issued tiles may be in flight
     const int last_issued = min(m + kAhead, ntiles - 1);
@@ -321,46 +376,24 @@ void attn_fwd_kernel(FwdParams p) {
   __syncthreads();
   if (!group_a) __syncthreads();
   if (ntiles > 0) {
-    mblock(0, 0, std::false_type{}, std::true_type{});
+    w.mblock<false, true>(kv_lds[0][1], kv_lds[0][0]);
     __syncthreads();
     if (group_a && kAhead < ntiles) issue_tile(kAhead);
-    softmax(0);
+    w.softmax(0, it.klen);
     if (group_a) wait_for_next(0);
     __syncthreads();
     for (int m = 1; m < ntiles; ++m) {
-      mblock(m - 1, m, std::true_type{}, std::true_type{});
+      w.mblock<true, true>(kv_lds[(m - 1) % kStages][1], kv_lds[m % kStages][0]);
       __syncthreads();
       if (group_a && m + kAhead < ntiles) issue_tile(m + kAhead);
-      softmax(m);
+      w.softmax(m * kBN, it.klen);
       if (group_a) wait_for_next(m);
       __syncthreads();
     }
-    mblock(ntiles - 1, ntiles - 1, std::true_type{}, std::false_type{});
+    w.mblock<true, false>(kv_lds[(ntiles - 1) % kStages][1], kv_lds[0][0]);
   }
   if (group_a) __syncthreads();
-
-  const float m_run = m_raw * c;
-  const float l_run = (l4[0] + l4[1]) + (l4[2] + l4[3]);
-
-  // Epilogue: normalise, optional padding correction, store O and LSE.
-  const float l_tot = pair_sum(l_run);
-  const bool any = l_tot > 0.f;
-  const float lse = any ? (m_run + __log2f(l_tot)) * kLn2 : -INFINITY;
-  float scale = any ? 1.0f / l_tot : 0.f;
-  if (p.ln_pad) scale *= 1.0f / (1.0f + expf(p.ln_pad[b] - lse));
-  if (qrow < p.Sq) {
-    bf16* op = p.o + b * p.os0 + (int64_t)qrow * p.os1 + h * p.os2 + 4 * hh;
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
-#pragma unroll
-      for (int rq = 0; rq < 4; ++rq) {
-        u32x2 w = {pack_bf16(o[dt][4 * rq] * scale, o[dt][4 * rq + 1] * scale),
-                   pack_bf16(o[dt][4 * rq + 2] * scale, o[dt][4 * rq + 3] * scale)};
-        *reinterpret_cast<u32x2*>(op + 32 * dt + 8 * rq) = w;
-      }
-    }
-    if (p.lse && hh == 0) p.lse[((int64_t)b * p.H + h) * p.Sq + qrow] = lse;
-  }
+  w.epilogue(p, it, qrow);
 }
 
 static bool stride_ok(const int64_t* s) {

@@ -72,6 +72,27 @@ def time_launches(fn, steps: int, warmup: int) -> tuple[float, float]:
     return wall, dev
 
 
+def time_graph(fn, reps: int = 20, replays: int = 5) -> float:
+    """Device ms per call of `fn` with host launch overhead removed: `reps` calls
+    captured into one HIP graph (on torch's capture stream), replayed `replays`
+    times between events. For ops whose GPU time is below the Python dispatch
+    time. `fn` must only launch kernels (no host syncs, no memsets)."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            fn()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(reps):
+            fn()
+    graph.replay()
+    torch.cuda.synchronize()
+    _, dev = time_launches(graph.replay, replays, 1)
+    return dev / reps
+
+
 def prewarm(fn, seconds: float = 0.5) -> None:
     """Runs `fn` for about `seconds` of wall time, so the GPU leaves its idle
     clock state before anything is timed (the first few ms after idle run
@@ -269,6 +290,53 @@ def main() -> int:
             "us": round(us_hn * 1e3, 2),
             "GB/s": round(2 * 2 * S * H * d * 2 / (us_hn * 1e-3) / 1e9, 1),
         }
+
+        # Configs 1 and 4 (§8(d) table): self-attention forward % of peak and the
+        # prologue's GB/s at B=1 S=1024 (launch-latency regime), B=16 S=4096 and
+        # B=1 S=9216 (96x96 latent).
+        fwd_nolse = torch.ops.anima_flat.fa_fwd_nolse
+        for name, (Bx, Sx, seed) in (("cfg1", (1, 1024, 1001)), ("cfg4a", (16, 4096, 1004)),
+                                     ("cfg4b", (1, 9216, 1014))):
+            px = prologue_qkv(pkg, Bx, Sx, H, seed, dev)
+            nsteps = steps if Bx * Sx * Sx <= 4096 * 4096 else max(5, steps // 4)
+            with torch.no_grad():
+                pro = lambda: pkg.qkv_norm_rope(px["qkv"], px["q_weight"], px["k_weight"], px["cos"],
+                                                px["sin"], H, eps)
+                _, us_p = time_launches(pro, nsteps, 3)
+                qx, kx, vx = pro()
+                attn_x = lambda: fwd_nolse(qx, kx, vx)
+                _, us_a = time_launches(attn_x, nsteps, 3)
+                small = Bx * Sx <= 1024  # GPU time below the op's Python dispatch time
+                if small:
+                    eager_a, eager_p = us_a, us_p
+                    us_a, us_p = time_graph(attn_x), time_graph(pro)
+            fl = attn_flops(Bx, H, Sx, Sx, d)
+            extras[f"self_{name}"] = {
+                "B": Bx, "seq_len": Sx, "us": round(us_a * 1e3, 2),
+                "TFLOP/s": round(fl / (us_a * 1e-3) / 1e12, 1),
+                "pct_of_peak": round(100 * fl / (us_a * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 2),
+            }
+            pb = 4 * Bx * Sx * H * d * 2 + 2 * Sx * 64 * 4  # read q,k sections; write q,k; tables
+            extras[f"prologue_{name}"] = {"us": round(us_p * 1e3, 2), "GB/s": round(pb / (us_p * 1e-3) / 1e9, 1)}
+            if small:
+                extras[f"self_{name}"]["timing"] = f"HIP graph of 20 calls; eager op {eager_a * 1e3:.1f} us"
+                extras[f"prologue_{name}"]["timing"] = f"HIP graph of 20 calls; eager op {eager_p * 1e3:.1f} us"
+            del px, qx, kx, vx
+        torch.cuda.empty_cache()
+
+        # Config 5 prologue under grad (V copied) and its backward.
+        qkv5 = p["qkv"].detach().clone().requires_grad_(True)
+        pro5 = lambda: pkg.qkv_norm_rope(qkv5, p["q_weight"], p["k_weight"], p["cos"], p["sin"], H, eps)
+        _, us_pf = time_launches(pro5, steps, 3)
+        gq, gk, gv = (torch.randn(B, S, H, d, device=dev, dtype=BF) for _ in range(3))
+        pro5_bwd = lambda: torch.ops.anima_flat.qkv_norm_rope_bwd(
+            p["qkv"], gq, gk, gv, p["q_weight"], p["k_weight"], p["cos"], p["sin"], H, eps)
+        _, us_pb = time_launches(pro5_bwd, steps, 3)
+        sec = B * S * H * d * 2  # one of q, k, v: bytes
+        extras["prologue_cfg5_fwd"] = {"us": round(us_pf * 1e3, 2),
+                                       "GB/s": round((6 * sec + 2 * S * 64 * 4) / (us_pf * 1e-3) / 1e9, 1)}
+        extras["prologue_cfg5_bwd"] = {"us": round(us_pb * 1e3, 2),
+                                       "GB/s": round((9 * sec + 2 * S * 64 * 4) / (us_pb * 1e-3) / 1e9, 1)}
 
         # Config 5: forward + backward (LoRA training attention), B=1, 4096.
         qg, kg, vg = (t.detach().clone().requires_grad_(True) for t in (q, k, v.contiguous()))

@@ -102,6 +102,36 @@ def test_attention_large_logits(pkg):
     parity(out, ref.attention_sdpa(q, k, v).reshape(B, S, H * 128), name="large logits")
 
 
+@pytest.mark.parametrize(
+    "B,Sq,Sk,H,lens",
+    [
+        (2, 4096, 160, 16, None),  # 512 work items: two rounds on 256 CUs
+        (1, 5120, 96, 15, None),  # 300 items: an uneven second round
+        (4, 4096, 300, 16, [0, 1, 65, 300]),  # 1024 items; a batch without keys, one key, partial tiles
+    ],
+)
+def test_large_grid_forward(pkg, B, Sq, Sk, H, lens):
+    """More work items (256 queries of one (batch, head)) than CUs (several
+    rounds of workgroups, an uneven last round), and a batch item with no keys."""
+    q, k, v = _qkv(B, Sq, Sk, H, seed=71 + B)
+    qd, kd, vd = _gpu(q, k, v)
+    if lens is None:
+        out, lse = torch.ops.anima_flat.fa_fwd(qd, kd, vd)
+        seq = None
+    else:
+        seq = torch.tensor(lens, dtype=torch.int32)
+        out, lse = torch.ops.anima_flat.fa_fwd_k(qd, kd, vd, seq.cuda())
+    torch.cuda.synchronize()
+    eo, el = ref.attention_lse(q, k, v, seq)
+    keep = [b for b in range(B) if lens is None or lens[b] > 0]
+    parity(out[keep], eo[keep], name=f"large grid out {B}x{Sq}x{Sk}x{H}")
+    parity(lse[keep], el[keep], **LSE_TOL, name=f"large grid lse {B}x{Sq}x{Sk}x{H}")
+    for b in range(B):
+        if lens is not None and lens[b] == 0:  # no keys: O = 0, LSE = -inf
+            assert torch.count_nonzero(out[b]).item() == 0
+            assert torch.isneginf(lse[b]).all()
+
+
 @pytest.mark.parametrize("lens", [[37, 80], [1, 64], [80, 80], [65, 3]])
 def test_masked_forward(pkg, lens):
     B, Sq, Sk, H = 2, 150, 80, 3
