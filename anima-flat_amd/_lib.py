@@ -17,7 +17,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().with_name("libanima_attn.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 AA_OK = 0
 AA_EINVAL = -1
@@ -48,6 +48,7 @@ _PROTOTYPES: dict[str, tuple[object, list[object]]] = {
         [c_void_p] * 5 + [c_void_p, c_size_t] + [_I64] * 4 + [c_float, c_int, c_void_p],
     ),
     "aa_attn_fwd": (c_int, [c_void_p, c_void_p]),
+    "aa_attn_fwd_workspace": (c_size_t, [_I64] * 5),
     "aa_attn_bwd_workspace": (c_size_t, [_I64] * 5),
     "aa_attn_bwd": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p]),
     "aa_ctx_scale_fwd": (c_int, [c_void_p] * 4 + [_I64] * 4 + [c_int, c_void_p]),
@@ -79,6 +80,8 @@ class AttnFwdArgs(Structure):
         ("hd", c_int64),
         ("softmax_scale", c_float),
         ("dtype", c_int),
+        ("workspace", c_void_p),
+        ("workspace_bytes", c_size_t),
     ]
 
 

@@ -130,6 +130,10 @@ def _launch_fwd(q, k, v, *, want_lse, seqused_k=None, ln_pad=None):
             raise ValueError(f"ln_pad must be [B]={B}, got {tuple(ln_pad.shape)}")
         ln_pad = ln_pad.to(device=q.device, dtype=torch.float32).contiguous()
     args = _fwd_args(q, k, v, out, lse, seqused_k, ln_pad)
+    ws_bytes = _lib.lib().aa_attn_fwd_workspace(B, Sq, k.shape[1], H, q.shape[3])
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None
+    if ws is not None:
+        args.workspace, args.workspace_bytes = ws.data_ptr(), ws_bytes
     _lib.call_attn_fwd(args, _lib.stream(q))
     return out, lse
 

@@ -39,6 +39,8 @@
 //   8/c (8 in log2 units), so p <= 256 and the O/l rescale (a pass over the
 //   64 accumulator registers) runs only a few times per row. The row sum is
 //   taken over the bf16-rounded P that feeds the MFMA, with v_dot2c_f32_bf16.
+#include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdlib>
 #include <type_traits>
@@ -65,6 +67,13 @@ struct FwdParams {
   int64_t os0, os1, os2;
   int H, Sq, Sk, nqblk, total_blocks;
   float c;  // softmax_scale * log2(e)
+  // Key split of the last work items (see split_plan): blocks past full_blocks
+  // each take one of nsplit key ranges of work item full_blocks + j / nsplit
+  // and write normalised fp32 partials (part_o [j][split][256][128],
+  // part_lse [j][split][256]) that attn_fwd_combine_kernel merges.
+  int full_blocks, split_items, nsplit;
+  float* part_o;
+  float* part_lse;
 };
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
@@ -293,6 +302,25 @@ struct FwdWave {
     }
   }
 
+  // Partial result of one key range: O / l in fp32 and the range's LSE, for
+  // the combine pass (no padding correction here). qloc = query in the item.
+  __device__ __forceinline__ void store_partial(const FwdParams& p, int64_t row, int qloc) const {
+    const float l_tot = pair_sum((l4[0] + l4[1]) + (l4[2] + l4[3]));
+    const bool any = l_tot > 0.f;
+    const float lse = any ? (m_raw * c + __log2f(l_tot)) * kLn2 : -INFINITY;
+    const float scale = any ? 1.0f / l_tot : 0.f;
+    float* op = p.part_o + (row * kQPerWg + qloc) * kD + 4 * hh;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int rq = 0; rq < 4; ++rq) {
+        const f32x4 v = {o[dt][4 * rq] * scale, o[dt][4 * rq + 1] * scale, o[dt][4 * rq + 2] * scale,
+                         o[dt][4 * rq + 3] * scale};
+        *reinterpret_cast<f32x4*>(op + 32 * dt + 8 * rq) = v;
+      }
+    if (hh == 0) p.part_lse[row * kQPerWg + qloc] = lse;
+  }
+
   // Normalise, optional padding correction, store O and LSE of query qrow.
   __device__ __forceinline__ void epilogue(const FwdParams& p, const Item& it, int qrow) const {
     const float m_run = m_raw * c;
@@ -337,20 +365,36 @@ struct FwdWave {
 // group B last read in phase 2m-1), and tile m+1 is complete before the
 // barrier that ends its X(m); the barriers order it for group B.
 //
-// One workgroup per work item (256 queries of one (batch, head)).
+// One workgroup per work item (256 queries of one (batch, head)), or per
+// key range of one of the last work items when they are split.
 __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_fwd_kernel(FwdParams p) {
   __shared__ __attribute__((aligned(1024))) bf16 kv_lds[kStages][2][kTileElems];
 
-  // Block -> work item, XCD-aware: the query blocks of one head share an XCD
-  // and its L2.
-  const Item it = decode_item(p, xcd_remap(blockIdx.x, p.total_blocks));
+  // Block -> work item, XCD-aware over the unsplit blocks: the query blocks
+  // of one head share an XCD and its L2.
+  int item_idx, split = -1;
+  if ((int)blockIdx.x < p.full_blocks) {
+    item_idx = xcd_remap(blockIdx.x, p.full_blocks);
+  } else {
+    const int j = blockIdx.x - p.full_blocks;
+    item_idx = p.full_blocks + j / p.nsplit;
+    split = j - (j / p.nsplit) * p.nsplit;
+  }
+  const Item it = decode_item(p, item_idx);
+  // Key tiles [t0, t0 + ntiles) of the item.
+  int t0 = 0, ntiles = it.ntiles;
+  if (split >= 0) {
+    const int per = (it.ntiles + p.nsplit - 1) / p.nsplit;
+    t0 = min(split * per, it.ntiles);
+    ntiles = min(per, it.ntiles - t0);
+  }
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const bool group_a = wave < 4;
   const int lane = tid & 63;
-  const int qrow = it.qblk * kQPerWg + wave * 32 + (lane & 31);
-  const int ntiles = it.ntiles;
+  const int qloc = wave * 32 + (lane & 31);
+  const int qrow = it.qblk * kQPerWg + qloc;
 
   FwdWave w;
   w.setup(lane, p.c);
@@ -361,7 +405,7 @@ void attn_fwd_kernel(FwdParams p) {
   const bf16* kp = p.k + it.b * p.ks0 + it.h * p.ks2;
   const bf16* vp = p.v + it.b * p.vs0 + it.h * p.vs2;
   auto issue_tile = [&](int t) {
-    dma.issue(p, kp, vp, it.klen, t, kv_lds[t % kStages][0], kv_lds[t % kStages][1]);
+    dma.issue(p, kp, vp, it.klen, t0 + t, kv_lds[t % kStages][0], kv_lds[t % kStages][1]);
   };
 
   static_assert(kAhead >= 1 && kAhead <= 4, "lookahead");
@@ -379,21 +423,65 @@ void attn_fwd_kernel(FwdParams p) {
     w.mblock<false, true>(kv_lds[0][1], kv_lds[0][0]);
     __syncthreads();
     if (group_a && kAhead < ntiles) issue_tile(kAhead);
-    w.softmax(0, it.klen);
+    w.softmax(t0 * kBN, it.klen);
     if (group_a) wait_for_next(0);
     __syncthreads();
     for (int m = 1; m < ntiles; ++m) {
       w.mblock<true, true>(kv_lds[(m - 1) % kStages][1], kv_lds[m % kStages][0]);
       __syncthreads();
       if (group_a && m + kAhead < ntiles) issue_tile(m + kAhead);
-      w.softmax(m * kBN, it.klen);
+      w.softmax((t0 + m) * kBN, it.klen);
       if (group_a) wait_for_next(m);
       __syncthreads();
     }
     w.mblock<true, false>(kv_lds[(ntiles - 1) % kStages][1], kv_lds[0][0]);
   }
   if (group_a) __syncthreads();
-  w.epilogue(p, it, qrow);
+  if (split < 0) w.epilogue(p, it, qrow);
+  else w.store_partial(p, (int64_t)(item_idx - p.full_blocks) * p.nsplit + split, qloc);
+}
+
+// Merges the key-range partials of the split work items: 8 queries per
+// workgroup, 32 lanes per query with 4 head-dim values each. O = sum_s
+// exp(lse_s - lse) O_s with lse = log sum_s exp(lse_s), then the optional
+// padding correction, bf16 O and LSE.
+__global__ __launch_bounds__(256) void attn_fwd_combine_kernel(FwdParams p) {
+  const int gq = blockIdx.x * 8 + (threadIdx.x >> 5);  // split-item query index
+  const int j = gq / kQPerWg, qloc = gq - j * kQPerWg;
+  if (j >= p.split_items) return;
+  const Item it = decode_item(p, p.full_blocks + j);
+  const int qrow = it.qblk * kQPerWg + qloc;
+  if (qrow >= p.Sq) return;
+  const int d0 = 4 * (threadIdx.x & 31);
+  const int64_t row0 = (int64_t)j * p.nsplit;
+  float ls[8];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    ls[s] = s < p.nsplit ? p.part_lse[(row0 + s) * kQPerWg + qloc] : -INFINITY;
+    mx = fmaxf(mx, ls[s]);
+  }
+  float lse = -INFINITY;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  if (mx > -INFINITY) {
+    float sum = 0.f;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) sum += expf(ls[s] - mx);
+    lse = mx + logf(sum);
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      if (s < p.nsplit && ls[s] > -INFINITY) {
+        const float wgt = expf(ls[s] - lse);
+        acc += wgt * ldf4(p.part_o + ((row0 + s) * kQPerWg + qloc) * kD + d0);
+      }
+    }
+  }
+  float scale = 1.f;
+  if (p.ln_pad) scale = 1.0f / (1.0f + expf(p.ln_pad[it.b] - lse));
+  bf16* op = p.o + it.b * p.os0 + (int64_t)qrow * p.os1 + it.h * p.os2 + d0;
+  const u32x2 w = {pack_bf16(acc[0] * scale, acc[1] * scale), pack_bf16(acc[2] * scale, acc[3] * scale)};
+  *reinterpret_cast<u32x2*>(op) = w;
+  if (p.lse && d0 == 0) p.lse[((int64_t)it.b * p.H + it.h) * p.Sq + qrow] = lse;
 }
 
 static bool stride_ok(const int64_t* s) {
@@ -403,6 +491,55 @@ static bool stride_ok(const int64_t* s) {
 }  // namespace aa
 
 using namespace aa;
+
+// Compute units of the current device (queried once per device).
+static int device_cu_count() {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int> cached[kMaxDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n > 0) return n;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  cached[dev].store(n, std::memory_order_relaxed);
+  return n;
+}
+
+// Key split of the work items of a partial last round. With T work items
+// on ncu CUs, the last T % ncu items would run alone on under half the chip;
+// when that is so, each of them is split into nsplit key ranges (up to 8, at
+// most one per key tile) so that they fill the CUs of that round.
+struct SplitPlan {
+  int full_blocks, split_items, nsplit;
+};
+
+static SplitPlan split_plan(int64_t T, int64_t Sk, int ncu) {
+  SplitPlan s{(int)T, 0, 1};
+  if (ncu <= 0 || T <= 0) return s;
+  const int64_t rem = T % ncu;
+  if (rem == 0 || 2 * rem > ncu) return s;
+  const int64_t ntk = (Sk + kBN - 1) / kBN;
+  const int ns = (int)std::min<int64_t>(std::min<int64_t>(8, ncu / rem), ntk);
+  if (ns < 2) return s;
+  s.full_blocks = (int)(T - rem);
+  s.split_items = (int)rem;
+  s.nsplit = ns;
+  return s;
+}
+
+static size_t split_workspace_bytes(const SplitPlan& s) {
+  return (size_t)s.split_items * s.nsplit * kQPerWg * (kD + 1) * sizeof(float);
+}
+
+static int64_t work_items(int64_t B, int64_t Sq, int64_t H) {
+  return B * H * ((Sq + kQPerWg - 1) / kQPerWg);
+}
+
+extern "C" size_t aa_attn_fwd_workspace(int64_t B, int64_t Sq, int64_t Sk, int64_t H, int64_t hd) {
+  (void)hd;
+  if (B <= 0 || Sq <= 0 || Sk <= 0 || H <= 0) return 0;
+  return split_workspace_bytes(split_plan(work_items(B, Sq, H), Sk, device_cu_count()));
+}
 
 // Validates args and fills the kernel parameters (no launch).
 static int prepare(const aa_attn_fwd_args* a, FwdParams& p) {
@@ -442,10 +579,21 @@ static int prepare(const aa_attn_fwd_args* a, FwdParams& p) {
   p.Sq = (int)a->Sq;
   p.Sk = (int)a->Sk;
   p.nqblk = (int)((a->Sq + kQPerWg - 1) / kQPerWg);
-  const int64_t total = a->B * a->H * p.nqblk;
-  if (total > 0x7fffffff) return fail(AA_EUNSUPPORTED, "attn_fwd: grid too large");
+  const int64_t total = work_items(a->B, a->Sq, a->H);
+  if (total > 0x7fffffff / 8) return fail(AA_EUNSUPPORTED, "attn_fwd: grid too large");
   p.total_blocks = (int)total;
   p.c = a->softmax_scale * kLog2e;
+  const SplitPlan sp = split_plan(total, a->Sk, device_cu_count());
+  const size_t ws_need = split_workspace_bytes(sp);
+  if (ws_need > 0 && (!a->workspace || a->workspace_bytes < ws_need))
+    return fail(AA_EINVAL, "attn_fwd: workspace too small (aa_attn_fwd_workspace)");
+  if (ws_need > 0 && !aligned16(a->workspace))
+    return fail(AA_EINVAL, "attn_fwd: workspace must be 16-byte aligned");
+  p.full_blocks = sp.full_blocks;
+  p.split_items = sp.split_items;
+  p.nsplit = sp.nsplit;
+  p.part_o = (float*)a->workspace;
+  p.part_lse = p.part_o + (size_t)sp.split_items * sp.nsplit * kQPerWg * kD;
   return AA_OK;
 }
 
@@ -455,6 +603,13 @@ extern "C" int aa_attn_fwd(const aa_attn_fwd_args* a, void* stream) {
   if (int rc = prepare(a, p)) return rc;
   if (a->B == 0 || a->Sq == 0) return AA_OK;
   hipStream_t st = (hipStream_t)stream;
-  attn_fwd_kernel<<<dim3((unsigned)p.total_blocks), kWaves * 64, 0, st>>>(p);
-  return check_launch("attn_fwd");
+  const int blocks = p.full_blocks + p.split_items * p.nsplit;
+  attn_fwd_kernel<<<dim3((unsigned)blocks), kWaves * 64, 0, st>>>(p);
+  if (int rc = check_launch("attn_fwd")) return rc;
+  if (p.split_items > 0) {
+    const int groups = (p.split_items * kQPerWg + 7) / 8;
+    attn_fwd_combine_kernel<<<dim3((unsigned)groups), 256, 0, st>>>(p);
+    return check_launch("attn_fwd combine");
+  }
+  return AA_OK;
 }

@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define AA_ABI_VERSION 2
+#define AA_ABI_VERSION 3
 
 enum {
   AA_OK = 0,
@@ -143,13 +143,20 @@ typedef struct aa_attn_fwd_args {
   int64_t B, Sq, Sk, H, hd;
   float softmax_scale;  /* usually 1/sqrt(hd) */
   int dtype;
+  void* workspace;      /* device scratch of aa_attn_fwd_workspace() bytes (may be 0) */
+  size_t workspace_bytes;
 } aa_attn_fwd_args;
+
+/* Bytes of device workspace aa_attn_fwd needs on the current device: fp32
+ * partial results when the work items (256 queries of one (batch, head)) of
+ * a partial last round of workgroups are split over key ranges, else 0. */
+size_t aa_attn_fwd_workspace(int64_t B, int64_t Sq, int64_t Sk, int64_t H, int64_t hd);
 
 /*
  * out = softmax(q k^T * softmax_scale) v, non-causal, per (batch, head);
  * keys j >= seqused_k[b] are excluded when seqused_k != NULL; lse is the
  * natural-log row log-sum-exp of the scaled scores over the attended keys.
- * One kernel launch, no device workspace.
+ * One kernel launch, plus a combine pass when aa_attn_fwd_workspace() > 0.
  * Replaces: src/attention.py:43-53 (anima_flat::fa_fwd),
  *           src/attention.py:63-66 (anima_flat::fa_fwd_nolse),
  *           src/attention.py:74-81 (anima_flat::fa_fwd_k), and with

@@ -46,6 +46,7 @@ def test_header_declares_the_entry_points():
         "aa_head_norm_fwd",
         "aa_head_norm_bwd",
         "aa_attn_fwd",
+        "aa_attn_fwd_workspace",
         "aa_attn_bwd",
         "aa_attn_bwd_workspace",
         "aa_ctx_scale_fwd",

@@ -108,6 +108,7 @@ def test_attention_large_logits(pkg):
         (2, 4096, 160, 16, None),  # 512 work items: two rounds on 256 CUs
         (1, 5120, 96, 15, None),  # 300 items: an uneven second round
         (4, 4096, 300, 16, [0, 1, 65, 300]),  # 1024 items; a batch without keys, one key, partial tiles
+        (2, 1024, 300, 8, [0, 170]),  # 64 items split over key ranges; empty ranges
     ],
 )
 def test_large_grid_forward(pkg, B, Sq, Sk, H, lens):
@@ -130,6 +131,20 @@ def test_large_grid_forward(pkg, B, Sq, Sk, H, lens):
         if lens is not None and lens[b] == 0:  # no keys: O = 0, LSE = -inf
             assert torch.count_nonzero(out[b]).item() == 0
             assert torch.isneginf(lse[b]).all()
+
+
+def test_forward_workspace(pkg):
+    """A partial last round of work items is split over key ranges (fp32
+    partials in the workspace); a whole number of rounds needs none."""
+    lib = pkg._lib.lib()
+    if torch.cuda.get_device_properties(0).multi_processor_count != 256:
+        pytest.skip("sizes below are for 256 CUs (MI355X)")
+    assert lib.aa_attn_fwd_workspace(1, 4096, 4096, 16, 128) == 0  # config 2: one full round
+    assert lib.aa_attn_fwd_workspace(2, 4096, 4096, 16, 128) == 0  # two full rounds
+    # config 1: 64 items alone on 256 CUs -> 4 key ranges each, 256 x (128 + 1) fp32 per range
+    assert lib.aa_attn_fwd_workspace(1, 1024, 1024, 16, 128) == 64 * 4 * 256 * 129 * 4
+    # config 4b: 576 items = 2 rounds + 64 -> the last 64 split 4 ways
+    assert lib.aa_attn_fwd_workspace(1, 9216, 9216, 16, 128) == 64 * 4 * 256 * 129 * 4
 
 
 @pytest.mark.parametrize("lens", [[37, 80], [1, 64], [80, 80], [65, 3]])
