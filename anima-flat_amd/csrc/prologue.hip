@@ -254,17 +254,28 @@ __global__ __launch_bounds__(kBwdThreads) void norm_bwd_kernel(
 }
 
 // Sums partial[nchunk][n] over chunks in a fixed order: 4 interleaved lanes of
-// chunks per output, combined in order. n <= 256.
+// chunks per output (chunks p, p + 4, ...), combined in order. The loads of
+// kBatch consecutive terms are issued together and then added in sequence, so
+// the chain of adds does not wait on one load at a time. n <= 256.
 __global__ __launch_bounds__(1024) void reduce_partials_kernel(const float* __restrict__ partial,
                                                                int64_t nchunk, int n,
                                                                float* __restrict__ out0,
                                                                float* __restrict__ out1) {
+  constexpr int kBatch = 16;
   __shared__ float red[4][256];
   const int o = threadIdx.x & 255;
   const int p = threadIdx.x >> 8;
   float s = 0.f;
   if (o < n) {
-    for (int64_t c = p; c < nchunk; c += 4) s += partial[c * n + o];
+    int64_t c = p;
+    for (; c + 4 * (kBatch - 1) < nchunk; c += 4 * kBatch) {
+      float t[kBatch];
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) t[i] = partial[(c + 4 * i) * n + o];
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) s += t[i];
+    }
+    for (; c < nchunk; c += 4) s += partial[c * n + o];
   }
   red[p][o] = s;
   __syncthreads();
@@ -283,7 +294,7 @@ __global__ void zero_f32_kernel(float* __restrict__ a, float* __restrict__ b, in
   }
 }
 
-constexpr int kBwdRows = 16;
+constexpr int kBwdRows = 4;  // tokens per block: enough blocks to keep the CUs' loads in flight
 
 static int64_t bwd_chunks(int64_t B, int64_t S) { return (B * S + kBwdRows - 1) / kBwdRows; }
 
