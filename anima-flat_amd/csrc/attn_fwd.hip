@@ -210,7 +210,9 @@ struct FwdWave {
   //   ops 16-31: S^T = K Q^T of the K tile ks, op = 16 + 2 kk + kt (A operand:
   //              one 16-byte read of the K tile; two accumulator chains s0, s1)
   // PV / QK select which half runs (the first tile has no PV, the tail no QK).
-  template <bool PV, bool QK, int kPrefetch = 12>
+  // A queue of 6 measured about 1% faster than 8, 10 or 12 at every shape
+  // tried (4096x4096, 9216x9216, 4096x512, 1024x1024) and needs fewer VGPRs.
+  template <bool PV, bool QK, int kPrefetch = 6>
   __device__ __forceinline__ void mblock(const bf16* vs, const bf16* ks) {
     constexpr int first = PV ? 0 : 16;
     constexpr int last = QK ? 32 : 16;
