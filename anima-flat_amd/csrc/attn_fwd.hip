@@ -25,6 +25,14 @@
 //   V^T operands are pairs of ds_read_b64_tr_b16 transposed reads. Both are
 //   free of bank conflicts.
 //
+// Q and O staging: each wave's 32 Q rows come in by DMA (4 rows x 256 B per
+//   instruction) into ring stages that the first tiles do not use, and are
+//   read into the Q^T registers from there; O leaves the same way, written to
+//   free ring stages and stored 4 whole rows per instruction. (Loading and
+//   storing straight from the accumulator layout touches 32 rows x 16-32 B
+//   per instruction; staging cut the fixed cost of a round of work items by
+//   about 5 us.)
+//
 // Key order of P^T
 //   The B operand of the MFMA wants, in lane l, 8 consecutive k-indices
 //   8*(l/32)+i of a 16-key chunk. The S^T accumulators hold, for that lane,
@@ -192,15 +200,26 @@ struct FwdWave {
     for (int i = 0; i < 4; ++i) l4[i] = 0.f;
   }
 
-  __device__ __forceinline__ void load_q(const FwdParams& p, const Item& it, int qrow,
-                                         bf16x8 (&dst)[8]) const {
-    const bf16* qp = p.q + it.b * p.qs0 + it.h * p.qs2 + (int64_t)qrow * p.qs1 + 8 * hh;
+  // Q rows of this wave's 32 queries (qrow0 ..) into its 8 KB of LDS, laid
+  // out like the O staging (chunk c of row r at slot c ^ (r & 15)): one DMA
+  // instruction per 4 rows, 256 contiguous bytes per row. Rows past Sq
+  // re-read row Sq - 1 (their results are never stored).
+  __device__ __forceinline__ void dma_q(const FwdParams& p, const Item& it, int qrow0, int lane,
+                                        bf16* stage) const {
+    const bf16* qp = p.q + it.b * p.qs0 + it.h * p.qs2;
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk) {
-      u32x4 w = {0u, 0u, 0u, 0u};
-      if (qrow < p.Sq) w = ld16(qp + 16 * kk);
-      dst[kk] = as_bf16x8(w);
+    for (int i = 0; i < 8; ++i) {
+      const int r = 4 * i + (lane >> 4);
+      const int row = min(qrow0 + r, p.Sq - 1);
+      const int ch = (lane & 15) ^ (r & 15);
+      dma16(qp + (int64_t)row * p.qs1 + 8 * ch, stage + 512 * i);
     }
+  }
+  // Q^T operands from the staged rows: qreg[kk] = row li, chunk 2 kk + hh.
+  __device__ __forceinline__ void read_q(const bf16* stage) {
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk)
+      qreg[kk] = *reinterpret_cast<const bf16x8*>(stage + li * 128 + (((2 * kk + hh) ^ (li & 15)) * 8));
   }
 
   // M block: up to 32 MFMAs in one unrolled stream, fed by a queue of LDS
@@ -305,26 +324,51 @@ struct FwdWave {
   }
 
   // Partial result of one key range: O / l in fp32 and the range's LSE, for
-  // the combine pass (no padding correction here). qloc = query in the item.
-  __device__ __forceinline__ void store_partial(const FwdParams& p, int64_t row, int qloc) const {
+  // the combine pass (no padding correction here). `row` is the (item,
+  // split) record; the wave holds queries qloc0 .. qloc0 + 31. Like O in the
+  // epilogue, the fp32 rows go through the wave's 8 KB of LDS, in two halves
+  // of 64 head-dim values (256 B per row), so that each store writes 4 whole
+  // 256-byte half rows.
+  __device__ __forceinline__ void store_partial(const FwdParams& p, int64_t row, int qloc0,
+                                                int lane, bf16* stage) const {
     const float l_tot = pair_sum((l4[0] + l4[1]) + (l4[2] + l4[3]));
     const bool any = l_tot > 0.f;
     const float lse = any ? (m_raw * c + __log2f(l_tot)) * kLn2 : -INFINITY;
     const float scale = any ? 1.0f / l_tot : 0.f;
-    float* op = p.part_o + (row * kQPerWg + qloc) * kD + 4 * hh;
+    float* fst = reinterpret_cast<float*>(stage);
+    float* op = p.part_o + (row * kQPerWg + qloc0) * kD;
+    const int ch = lane & 15;
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
+    for (int half = 0; half < 2; ++half) {
 #pragma unroll
-      for (int rq = 0; rq < 4; ++rq) {
-        const f32x4 v = {o[dt][4 * rq] * scale, o[dt][4 * rq + 1] * scale, o[dt][4 * rq + 2] * scale,
-                         o[dt][4 * rq + 3] * scale};
-        *reinterpret_cast<f32x4*>(op + 32 * dt + 8 * rq) = v;
+      for (int dh = 0; dh < 2; ++dh) {
+        const int dt = 2 * half + dh;
+#pragma unroll
+        for (int rq = 0; rq < 4; ++rq) {
+          // 4 floats at d = 32 dt + 8 rq + 4 hh: 16-byte chunk 8 dh + 2 rq + hh of the half row.
+          const f32x4 v = {o[dt][4 * rq] * scale, o[dt][4 * rq + 1] * scale,
+                           o[dt][4 * rq + 2] * scale, o[dt][4 * rq + 3] * scale};
+          const int c16 = 8 * dh + 2 * rq + hh;
+          *reinterpret_cast<f32x4*>(fst + li * 64 + ((c16 ^ (li & 15)) * 4)) = v;
+        }
       }
-    if (hh == 0) p.part_lse[row * kQPerWg + qloc] = lse;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int r = (lane >> 4) + 4 * i;
+        const f32x4 v = *reinterpret_cast<const f32x4*>(fst + r * 64 + ((ch ^ (r & 15)) * 4));
+        *reinterpret_cast<f32x4*>(op + r * kD + 64 * half + 4 * ch) = v;
+      }
+    }
+    if (hh == 0) p.part_lse[row * kQPerWg + qloc0 + li] = lse;
   }
 
   // Normalise, optional padding correction, store O and LSE of query qrow.
-  __device__ __forceinline__ void epilogue(const FwdParams& p, const Item& it, int qrow) const {
+  // O goes through this wave's 8 KB of LDS (stage: 32 rows x 256 B, the
+  // 16-byte chunk c of row r at slot c ^ (r & 15), conflict free both ways)
+  // so that each global store writes 4 whole 256-byte rows.
+  __device__ __forceinline__ void epilogue(const FwdParams& p, const Item& it, int qrow0, int lane,
+                                           bf16* stage) const {
+    const int qrow = qrow0 + li;
     const float m_run = m_raw * c;
     const float l_run = (l4[0] + l4[1]) + (l4[2] + l4[3]);
     const float l_tot = pair_sum(l_run);
@@ -332,18 +376,24 @@ struct FwdWave {
     const float lse = any ? (m_run + __log2f(l_tot)) * kLn2 : -INFINITY;
     float scale = any ? 1.0f / l_tot : 0.f;
     if (p.ln_pad) scale *= 1.0f / (1.0f + expf(p.ln_pad[it.b] - lse));
-    if (qrow < p.Sq) {
-      bf16* op = p.o + it.b * p.os0 + (int64_t)qrow * p.os1 + it.h * p.os2 + 4 * hh;
 #pragma unroll
-      for (int dt = 0; dt < 4; ++dt) {
+    for (int dt = 0; dt < 4; ++dt) {
 #pragma unroll
-        for (int rq = 0; rq < 4; ++rq) {
-          u32x2 w = {pack_bf16(o[dt][4 * rq] * scale, o[dt][4 * rq + 1] * scale),
-                     pack_bf16(o[dt][4 * rq + 2] * scale, o[dt][4 * rq + 3] * scale)};
-          *reinterpret_cast<u32x2*>(op + 32 * dt + 8 * rq) = w;
-        }
+      for (int rq = 0; rq < 4; ++rq) {
+        const u32x2 w = {pack_bf16(o[dt][4 * rq] * scale, o[dt][4 * rq + 1] * scale),
+                         pack_bf16(o[dt][4 * rq + 2] * scale, o[dt][4 * rq + 3] * scale)};
+        const int ch = 4 * dt + rq;
+        *reinterpret_cast<u32x2*>(stage + li * 128 + ((ch ^ (li & 15)) * 8) + 4 * hh) = w;
       }
-      if (p.lse && hh == 0) p.lse[((int64_t)it.b * p.H + it.h) * p.Sq + qrow] = lse;
+    }
+    if (p.lse && hh == 0 && qrow < p.Sq) p.lse[((int64_t)it.b * p.H + it.h) * p.Sq + qrow] = lse;
+    const int ch = lane & 15;
+    bf16* ob = p.o + it.b * p.os0 + it.h * p.os2 + 8 * ch;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int r = (lane >> 4) + 4 * i;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(stage + r * 128 + ((ch ^ (r & 15)) * 8));
+      if (qrow0 + r < p.Sq) st16(ob + (int64_t)(qrow0 + r) * p.os1, v);
     }
   }
 };
@@ -400,7 +450,10 @@ void attn_fwd_kernel(FwdParams p) {
 
   FwdWave w;
   w.setup(lane, p.c);
-  w.load_q(p, it, qrow, w.qreg);
+  // Q rows staged in ring stages 2 and 3 (free until tile 2's DMA, which
+  // group A issues after the first barrier that follows every wave's read).
+  bf16* qstage = &kv_lds[2 + (wave >> 2)][0][0] + (wave & 3) * 4096;
+  w.dma_q(p, it, qrow - (lane & 31), lane, qstage);
   w.reset();
   KVDma dma;
   dma.setup(p, wave, lane);
@@ -417,8 +470,11 @@ void attn_fwd_kernel(FwdParams p) {
   };
   if (group_a && ntiles > 0) {
     for (int t = 0; t < kAhead && t < ntiles; ++t) issue_tile(t);
-    wait_for_next(-1);
+    wait_for_next(-1);  // also the Q rows, issued before
+  } else {
+    wait_dma();
   }
+  w.read_q(qstage);
   __syncthreads();
   if (!group_a) __syncthreads();
   if (ntiles > 0) {
@@ -439,8 +495,12 @@ void attn_fwd_kernel(FwdParams p) {
     w.mblock<true, false>(kv_lds[(ntiles - 1) % kStages][1], kv_lds[0][0]);
   }
   if (group_a) __syncthreads();
-  if (split < 0) w.epilogue(p, it, qrow);
-  else w.store_partial(p, (int64_t)(item_idx - p.full_blocks) * p.nsplit + split, qloc);
+  // Output staging: the two stages after the last tile's are free (group B
+  // may still be reading the last tile's V in its final M block; nothing else
+  // is read or in flight).
+  bf16* stage = &kv_lds[(ntiles + (wave >> 2)) % kStages][0][0] + (wave & 3) * 4096;
+  if (split < 0) w.epilogue(p, it, qrow - (lane & 31), lane, stage);
+  else w.store_partial(p, (int64_t)(item_idx - p.full_blocks) * p.nsplit + split, wave * 32, lane, stage);
 }
 
 // Merges the key-range partials of the split work items: 8 queries per
