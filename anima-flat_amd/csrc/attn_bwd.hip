@@ -135,20 +135,15 @@ void dkdv_kernel(Params p, int nkblk, int total_blocks) {
   const int li = lane & 31, hh = lane >> 5;
 
   // B operand of the role's S / dP product: lane holds K (A) or V (B)
-  // [key][16 kk + 8 hh + 0..7].
-  const int key = kblk * kKeysPerWg + pair * 32 + li;
-  const bool key_ok = key < p.Sk;
+  // [key][16 kk + 8 hh + 0..7], read from the wave's rows staged in LDS
+  // (tile_io.h) in ring stages 2 and 3, which the first query tiles' DMA
+  // leaves alone until after the first barrier. Keys past Sk re-read key
+  // Sk - 1: their accumulators are never stored.
+  const int key0 = kblk * kKeysPerWg + pair * 32;
   bf16x8 kv[8];
-  {
-    const bf16* src = role_a ? p.k + b * p.s_k[0] + h * p.s_k[2] + (int64_t)key * p.s_k[1]
-                             : p.v + b * p.s_v[0] + h * p.s_v[2] + (int64_t)key * p.s_v[1];
-#pragma unroll
-    for (int kk = 0; kk < 8; ++kk) {
-      u32x4 w = {0u, 0u, 0u, 0u};
-      if (key_ok) w = ld16(src + 8 * hh + 16 * kk);
-      kv[kk] = as_bf16x8(w);
-    }
-  }
+  const bf16* kvstage = &rows[2 + (wave >> 2)][0][0] + (wave & 3) * 4096;
+  if (role_a) stage_rows_in(p.k + b * p.s_k[0] + h * p.s_k[2], p.s_k[1], key0, p.Sk, lane, kvstage);
+  else stage_rows_in(p.v + b * p.s_v[0] + h * p.s_v[2], p.s_v[1], key0, p.Sk, lane, kvstage);
 
   const bf16* qbase = p.q + b * p.s_q[0] + h * p.s_q[2];
   const bf16* dobase = p.dout + b * p.s_do[0] + h * p.s_do[2];
@@ -276,10 +271,10 @@ void dkdv_kernel(Params p, int nkblk, int total_blocks) {
       wait_dma();
     }
   };
-  if (ntiles > 0 && !role_a) {
-    issue_tile(0);
-    wait_dma();
-  }
+  if (ntiles > 0 && !role_a) issue_tile(0);
+  wait_dma();  // the staged K / V rows (and tile 0)
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk) kv[kk] = staged_operand(kvstage, lane, kk);
   __syncthreads();
   if (ntiles > 0) {
     if (!role_a) {  // the DMA of X_B(-2) and X_B(-1), then the phase shift
@@ -303,22 +298,13 @@ void dkdv_kernel(Params p, int nkblk, int total_blocks) {
     if (role_a) __syncthreads();
   }
 
-  if (key_ok) {
-    bf16* dst = role_a ? p.dv + b * p.s_dv[0] + (int64_t)key * p.s_dv[1] + h * p.s_dv[2]
-                       : p.dk + b * p.s_dk[0] + (int64_t)key * p.s_dk[1] + h * p.s_dk[2];
-    const float sc = role_a ? 1.0f : p.scale;
-    dst += 4 * hh;
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
-#pragma unroll
-      for (int rq = 0; rq < 4; ++rq) {
-        const f32x16& a = acc[dt];
-        u32x2 w = {pack_bf16(a[4 * rq] * sc, a[4 * rq + 1] * sc),
-                   pack_bf16(a[4 * rq + 2] * sc, a[4 * rq + 3] * sc)};
-        *reinterpret_cast<u32x2*>(dst + 32 * dt + 8 * rq) = w;
-      }
-    }
-  }
+  // dV (A) / dK (B) rows out through LDS staging: the stages of tiles
+  // ntiles-4 and ntiles-3 are free (B may still be reading tile ntiles-1 in
+  // its final M block; no DMA is in flight).
+  bf16* ostage = &rows[(ntiles + (wave >> 2)) % kDkStages][0][0] + (wave & 3) * 4096;
+  stage_acc_rows(acc, role_a ? 1.0f : p.scale, lane, ostage);
+  if (role_a) stage_rows_out(p.dv + b * p.s_dv[0] + h * p.s_dv[2], p.s_dv[1], key0, p.Sk, lane, ostage);
+  else stage_rows_out(p.dk + b * p.s_dk[0] + h * p.s_dk[2], p.s_dk[1], key0, p.Sk, lane, ostage);
 }
 
 // ------------------------------------------------------------------ dQ --
@@ -508,19 +494,13 @@ void dq_kernel(Params p, int nqblk, int total_blocks) {
   }
   if (group_a) __syncthreads();
 
-  if (q_ok) {
-    bf16* dqp = p.dq + b * p.s_dq[0] + (int64_t)qrow * p.s_dq[1] + h * p.s_dq[2] + 4 * hh;
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
-#pragma unroll
-      for (int rq = 0; rq < 4; ++rq) {
-        const f32x16& a = dq[dt];
-        u32x2 w = {pack_bf16(a[4 * rq] * p.scale, a[4 * rq + 1] * p.scale),
-                   pack_bf16(a[4 * rq + 2] * p.scale, a[4 * rq + 3] * p.scale)};
-        *reinterpret_cast<u32x2*>(dqp + 32 * dt + 8 * rq) = w;
-      }
-    }
-  }
+  // dQ rows out through LDS staging in the stages of tiles ntiles-4 and
+  // ntiles-3 (free: group B may still be reading tile ntiles-1 in its final
+  // M block; no DMA is in flight).
+  bf16* ostage = &tiles[(ntiles + (wave >> 2)) % kDqStages][0][0] + (wave & 3) * 4096;
+  stage_acc_rows(dq, p.scale, lane, ostage);
+  stage_rows_out(p.dq + b * p.s_dq[0] + h * p.s_dq[2], p.s_dq[1], qblk * kQueriesPerWg + wave * 32,
+                 p.Sq, lane, ostage);
 }
 
 static bool stride_ok(const int64_t* s) {

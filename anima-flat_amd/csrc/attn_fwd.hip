@@ -200,26 +200,17 @@ struct FwdWave {
     for (int i = 0; i < 4; ++i) l4[i] = 0.f;
   }
 
-  // Q rows of this wave's 32 queries (qrow0 ..) into its 8 KB of LDS, laid
-  // out like the O staging (chunk c of row r at slot c ^ (r & 15)): one DMA
-  // instruction per 4 rows, 256 contiguous bytes per row. Rows past Sq
-  // re-read row Sq - 1 (their results are never stored).
+  // Q rows of this wave's 32 queries (qrow0 ..) into its 8 KB of LDS
+  // (tile_io.h row staging); rows past Sq re-read row Sq - 1 (their results
+  // are never stored).
   __device__ __forceinline__ void dma_q(const FwdParams& p, const Item& it, int qrow0, int lane,
-                                        bf16* stage) const {
-    const bf16* qp = p.q + it.b * p.qs0 + it.h * p.qs2;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int r = 4 * i + (lane >> 4);
-      const int row = min(qrow0 + r, p.Sq - 1);
-      const int ch = (lane & 15) ^ (r & 15);
-      dma16(qp + (int64_t)row * p.qs1 + 8 * ch, stage + 512 * i);
-    }
+                                        const bf16* stage) const {
+    stage_rows_in(p.q + it.b * p.qs0 + it.h * p.qs2, p.qs1, qrow0, p.Sq, lane, stage);
   }
   // Q^T operands from the staged rows: qreg[kk] = row li, chunk 2 kk + hh.
-  __device__ __forceinline__ void read_q(const bf16* stage) {
+  __device__ __forceinline__ void read_q(const bf16* stage, int lane) {
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk)
-      qreg[kk] = *reinterpret_cast<const bf16x8*>(stage + li * 128 + (((2 * kk + hh) ^ (li & 15)) * 8));
+    for (int kk = 0; kk < 8; ++kk) qreg[kk] = staged_operand(stage, lane, kk);
   }
 
   // M block: up to 32 MFMAs in one unrolled stream, fed by a queue of LDS
@@ -362,10 +353,9 @@ struct FwdWave {
     if (hh == 0) p.part_lse[row * kQPerWg + qloc0 + li] = lse;
   }
 
-  // Normalise, optional padding correction, store O and LSE of query qrow.
-  // O goes through this wave's 8 KB of LDS (stage: 32 rows x 256 B, the
-  // 16-byte chunk c of row r at slot c ^ (r & 15), conflict free both ways)
-  // so that each global store writes 4 whole 256-byte rows.
+  // Normalise, optional padding correction, store O and LSE of queries
+  // qrow0 .. qrow0 + 31. O goes out through this wave's 8 KB of LDS (tile_io.h
+  // row staging), 4 whole 256-byte rows per store.
   __device__ __forceinline__ void epilogue(const FwdParams& p, const Item& it, int qrow0, int lane,
                                            bf16* stage) const {
     const int qrow = qrow0 + li;
@@ -376,25 +366,9 @@ struct FwdWave {
     const float lse = any ? (m_run + __log2f(l_tot)) * kLn2 : -INFINITY;
     float scale = any ? 1.0f / l_tot : 0.f;
     if (p.ln_pad) scale *= 1.0f / (1.0f + expf(p.ln_pad[it.b] - lse));
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
-#pragma unroll
-      for (int rq = 0; rq < 4; ++rq) {
-        const u32x2 w = {pack_bf16(o[dt][4 * rq] * scale, o[dt][4 * rq + 1] * scale),
-                         pack_bf16(o[dt][4 * rq + 2] * scale, o[dt][4 * rq + 3] * scale)};
-        const int ch = 4 * dt + rq;
-        *reinterpret_cast<u32x2*>(stage + li * 128 + ((ch ^ (li & 15)) * 8) + 4 * hh) = w;
-      }
-    }
+    stage_acc_rows(o, scale, lane, stage);
     if (p.lse && hh == 0 && qrow < p.Sq) p.lse[((int64_t)it.b * p.H + it.h) * p.Sq + qrow] = lse;
-    const int ch = lane & 15;
-    bf16* ob = p.o + it.b * p.os0 + it.h * p.os2 + 8 * ch;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int r = (lane >> 4) + 4 * i;
-      const u32x4 v = *reinterpret_cast<const u32x4*>(stage + r * 128 + ((ch ^ (r & 15)) * 8));
-      if (qrow0 + r < p.Sq) st16(ob + (int64_t)(qrow0 + r) * p.os1, v);
-    }
+    stage_rows_out(p.o + it.b * p.os0 + it.h * p.os2, p.os1, qrow0, p.Sq, lane, stage);
   }
 };
 
@@ -474,7 +448,7 @@ void attn_fwd_kernel(FwdParams p) {
   } else {
     wait_dma();
   }
-  w.read_q(qstage);
+  w.read_q(qstage, lane);
   __syncthreads();
   if (!group_a) __syncthreads();
   if (ntiles > 0) {

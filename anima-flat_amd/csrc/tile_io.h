@@ -113,6 +113,64 @@ __device__ __forceinline__ bf16x8 read_tr_operand(const bf16* tile, int c4, int 
   return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
+// Wave-private row staging -----------------------------------------------------
+//
+// 32 rows x 128 bf16 (8 KB) per wave, 16-byte chunk c of row r at element
+// r * 128 + ((c ^ (r & 15)) * 8). Rows move between HBM and the staging area
+// 4 whole 256-byte rows per instruction (DMA in, 16-byte stores out), and
+// lanes read or write them in the MFMA register layouts (lane li = lane % 32
+// is row li) without bank conflicts: 16 lanes on one chunk of 16 rows hit 16
+// distinct slots. Loading or storing the register layouts straight from HBM
+// touches 32 rows x 16-32 B per instruction instead.
+
+__device__ __forceinline__ int stage_at(int r, int c) { return r * 128 + ((c ^ (r & 15)) * 8); }
+
+// DMA of rows row0 .. row0 + 31 (row stride rs) into the staging area; rows
+// at or past nrows (>= 1) re-read row nrows - 1.
+__device__ __forceinline__ void stage_rows_in(const bf16* base, int64_t rs, int row0, int nrows,
+                                              int lane, const bf16* stage) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int r = 4 * i + (lane >> 4);
+    const int row = min(row0 + r, nrows - 1);
+    const int c = (lane & 15) ^ (r & 15);
+    dma16(base + (int64_t)row * rs + 8 * c, stage + 512 * i);
+  }
+}
+
+// Row operand kk of staged row li: elements 16 kk + 8 hh .. + 7.
+__device__ __forceinline__ bf16x8 staged_operand(const bf16* stage, int lane, int kk) {
+  const int li = lane & 31, hh = lane >> 5;
+  return *reinterpret_cast<const bf16x8*>(stage + stage_at(li, 2 * kk + hh));
+}
+
+// Four 32x32 accumulators acc[dt] holding [d = 32 dt + 8 (r / 4) + 4 hh + r % 4]
+// [row li] (register r), times scale, as bf16 rows into the staging area.
+__device__ __forceinline__ void stage_acc_rows(const f32x16 (&acc)[4], float scale, int lane,
+                                               bf16* stage) {
+  const int li = lane & 31, hh = lane >> 5;
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+    for (int rq = 0; rq < 4; ++rq) {
+      const u32x2 w = {pack_bf16(acc[dt][4 * rq] * scale, acc[dt][4 * rq + 1] * scale),
+                       pack_bf16(acc[dt][4 * rq + 2] * scale, acc[dt][4 * rq + 3] * scale)};
+      *reinterpret_cast<u32x2*>(stage + stage_at(li, 4 * dt + rq) + 4 * hh) = w;
+    }
+}
+
+// Staged rows r with row0 + r < nrows to base + (row0 + r) * rs.
+__device__ __forceinline__ void stage_rows_out(bf16* base, int64_t rs, int row0, int nrows,
+                                               int lane, const bf16* stage) {
+  const int c = lane & 15;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int r = (lane >> 4) + 4 * i;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(stage + stage_at(r, c));
+    if (row0 + r < nrows) st16(base + (int64_t)(row0 + r) * rs + 8 * c, v);
+  }
+}
+
 // Workgroups are dispatched round-robin over the 8 XCDs (block i on XCD
 // i % 8). Remap so each XCD gets a contiguous range of logical blocks, whose
 // shared K/V (or Q/dO) rows then stay in that XCD's L2.
