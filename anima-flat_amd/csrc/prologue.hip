@@ -253,6 +253,25 @@ __global__ __launch_bounds__(kBwdThreads) void norm_bwd_kernel(
   }
 }
 
+// First level of the weight-gradient reduction: block i sums chunks
+// kL1Chunks i .. kL1Chunks i + kL1Chunks - 1 of partial[nchunk][n] in order
+// into l1[i][n] (n <= 256, one thread per output, coalesced rows).
+constexpr int kL1Chunks = 16;
+__global__ __launch_bounds__(256) void reduce_partials_l1_kernel(const float* __restrict__ partial,
+                                                                 int64_t nchunk, int n,
+                                                                 float* __restrict__ l1) {
+  const int o = threadIdx.x;
+  if (o >= n) return;
+  const int64_t c0 = (int64_t)blockIdx.x * kL1Chunks;
+  float t[kL1Chunks];
+#pragma unroll
+  for (int i = 0; i < kL1Chunks; ++i) t[i] = c0 + i < nchunk ? partial[(c0 + i) * n + o] : 0.f;
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < kL1Chunks; ++i) s += t[i];
+  l1[(int64_t)blockIdx.x * n + o] = s;
+}
+
 // Sums partial[nchunk][n] over chunks in a fixed order: 4 interleaved lanes of
 // chunks per output (chunks p, p + 4, ...), combined in order. The loads of
 // kBatch consecutive terms are issued together and then added in sequence, so
@@ -297,6 +316,23 @@ __global__ void zero_f32_kernel(float* __restrict__ a, float* __restrict__ b, in
 constexpr int kBwdRows = 4;  // tokens per block: enough blocks to keep the CUs' loads in flight
 
 static int64_t bwd_chunks(int64_t B, int64_t S) { return (B * S + kBwdRows - 1) / kBwdRows; }
+static int64_t l1_blocks(int64_t nchunk) { return (nchunk + kL1Chunks - 1) / kL1Chunks; }
+
+// Weight-gradient workspace: the per-chunk partials, then the first-level sums.
+static size_t wgrad_workspace(int64_t B, int64_t S, int64_t n) {
+  const int64_t nchunk = bwd_chunks(B, S);
+  return (size_t)(nchunk + l1_blocks(nchunk)) * (size_t)n * sizeof(float);
+}
+
+// Two-level fixed-order sum of partial[nchunk][n] into out0 / out1 (outputs
+// 0..127 / 128..255).
+static void reduce_wgrad(float* partial, int64_t nchunk, int n, float* out0, float* out1,
+                         hipStream_t st) {
+  float* l1 = partial + nchunk * n;
+  const int64_t nl1 = l1_blocks(nchunk);
+  reduce_partials_l1_kernel<<<dim3((unsigned)nl1), 256, 0, st>>>(partial, nchunk, n, l1);
+  reduce_partials_kernel<<<1, 1024, 0, st>>>(l1, nl1, n, out0, out1);
+}
 
 static int check_common(int64_t B, int64_t S, int64_t H, int64_t hd, int dtype) {
   if (dtype != AA_DTYPE_BF16) return fail(AA_EUNSUPPORTED, "only bf16 activations are implemented");
@@ -354,12 +390,12 @@ extern "C" int aa_head_norm_fwd(const void* x, void* y, const float* weight, int
 
 extern "C" size_t aa_qkv_norm_rope_bwd_workspace(int64_t B, int64_t S, int64_t H, int64_t hd) {
   (void)H;
-  return (size_t)bwd_chunks(B, S) * 2 * (size_t)hd * sizeof(float);
+  return wgrad_workspace(B, S, 2 * hd);
 }
 
 extern "C" size_t aa_head_norm_bwd_workspace(int64_t B, int64_t S, int64_t H, int64_t hd) {
   (void)H;
-  return (size_t)bwd_chunks(B, S) * (size_t)hd * sizeof(float);
+  return wgrad_workspace(B, S, hd);
 }
 
 extern "C" int aa_qkv_norm_rope_bwd(const void* qkv, const void* dq, const void* dk,
@@ -390,7 +426,7 @@ extern "C" int aa_qkv_norm_rope_bwd(const void* qkv, const void* dq, const void*
       (const bf16*)qkv, (const bf16*)dq, (const bf16*)dk, (const bf16*)dv, (bf16*)dqkv,
       q_weight, k_weight, cos, sin, partial, B * S, S, (int)H, kBwdRows, eps);
   if (int rc = check_launch("qkv_norm_rope_bwd")) return rc;
-  reduce_partials_kernel<<<1, 1024, 0, st>>>(partial, nchunk, 2 * kHd, dq_weight, dk_weight);
+  reduce_wgrad(partial, nchunk, 2 * kHd, dq_weight, dk_weight, st);
   return check_launch("qkv_norm_rope_bwd reduce");
 }
 
@@ -416,6 +452,6 @@ extern "C" int aa_head_norm_bwd(const void* x, const void* dy, void* dx, const f
       (const bf16*)x, (const bf16*)dy, nullptr, nullptr, (bf16*)dx, weight, weight, nullptr,
       nullptr, partial, B * S, S, (int)H, kBwdRows, eps);
   if (int rc = check_launch("head_norm_bwd")) return rc;
-  reduce_partials_kernel<<<1, 1024, 0, st>>>(partial, nchunk, kHd, dweight, dweight);
+  reduce_wgrad(partial, nchunk, kHd, dweight, dweight, st);
   return check_launch("head_norm_bwd reduce");
 }

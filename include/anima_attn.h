@@ -89,7 +89,8 @@ int aa_head_norm_fwd(const void* x, void* y, const float* weight,
                      int64_t B, int64_t S, int64_t H, int64_t hd,
                      float eps, int dtype, void* stream);
 
-/* Bytes of workspace aa_qkv_norm_rope_bwd needs (weight-grad partials). */
+/* Bytes of workspace aa_qkv_norm_rope_bwd needs (weight-grad partials: one
+ * 2*hd float record per 4 tokens, then one per 16 such records). */
 size_t aa_qkv_norm_rope_bwd_workspace(int64_t B, int64_t S, int64_t H, int64_t hd);
 
 /*
@@ -109,7 +110,7 @@ int aa_qkv_norm_rope_bwd(const void* qkv, const void* dq, const void* dk,
                          int64_t B, int64_t S, int64_t H, int64_t hd,
                          float eps, int dtype, void* stream);
 
-/* Bytes of workspace aa_head_norm_bwd needs. */
+/* Bytes of workspace aa_head_norm_bwd needs (as above with hd floats). */
 size_t aa_head_norm_bwd_workspace(int64_t B, int64_t S, int64_t H, int64_t hd);
 
 /*

@@ -89,8 +89,9 @@ def test_workspace_sizes(lib):
     assert lib.aa_attn_bwd_workspace(2, 100, 77, 3, 128) == 2 * 3 * 2 * 1024
     assert lib.aa_attn_bwd_workspace(1, 0, 77, 3, 128) == 0
     # weight-gradient partials: one [2][128] (or [128]) fp32 record per 4 tokens
-    assert lib.aa_qkv_norm_rope_bwd_workspace(1, 4096, 16, 128) == 1024 * 2 * 128 * 4
-    assert lib.aa_head_norm_bwd_workspace(2, 9, 5, 128) == 5 * 128 * 4
+    # One record per 4 tokens, then one per 16 records (the two-level reduction).
+    assert lib.aa_qkv_norm_rope_bwd_workspace(1, 4096, 16, 128) == (1024 + 64) * 2 * 128 * 4
+    assert lib.aa_head_norm_bwd_workspace(2, 9, 5, 128) == (5 + 1) * 128 * 4
 
 
 def test_invalid_arguments_fail_before_any_launch(pkg, lib):
