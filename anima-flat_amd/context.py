@@ -5,6 +5,10 @@ Mirrors the parts of anima-flat's src/model.py that feed the path:
   Context          <- model.py:87-119 (per-layer K/V + trim state, `attend`)
   trim_context     <- model.py:247-254 (drop trailing zero padding of the text
                       context; key lengths and log of the removed padding)
+  context_lengths  <- model.py:248-253 on the device (aa_context_lengths): the
+                      same key lengths and log padding with no host read and no
+                      trim (the masked attention reads only the first
+                      seqused[b] keys of the untrimmed K/V)
 
 The table formula must reproduce the reference's values exactly, so it
 follows the same sequence of float32 operations.
@@ -14,7 +18,9 @@ from __future__ import annotations
 
 import torch
 
+from . import _lib
 from .attention import attention, cross_attention_trimmed
+from .kernels.common import _check
 
 
 def rope_tables(
@@ -98,3 +104,46 @@ def trim_context(ctx: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.T
     seqused = lengths.to(torch.int32).contiguous()
     ln_pad = torch.log((S - lengths).float())
     return ctx[:, :keep], seqused, ln_pad
+
+
+_ELEM_BYTES = {torch.bfloat16: 2, torch.float16: 2, torch.float32: 4}
+
+
+def context_lengths(ctx: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Key lengths and log padding of a zero-padded text context, on the GPU.
+
+    The same values as `trim_context` (length of item b = 1-based index of its
+    last row with a non-zero element, at least 1; ln_pad = log(S - length)),
+    computed by one HIP pass over `ctx` with no device-to-host read. The
+    context is not trimmed: K/V projected from all S rows go to
+    `cross_attention_trimmed` / `Context` with these values, and the masked
+    attention reads only the first `seqused[b]` keys, so the result equals
+    the reference's trimmed path (model.py:247-254) without its sync.
+
+    Args:
+        ctx: `[B, S, C]` bf16, fp16 or fp32 CUDA tensor, last dim contiguous,
+            rows 16-byte aligned (C * element size a multiple of 16 bytes).
+
+    Returns:
+        `(seqused int32 [B], ln_pad float32 [B])` on ctx's device.
+    """
+    _check(ctx)
+    if ctx.dim() != 3 or ctx.stride(2) != 1:
+        raise ValueError("context_lengths: ctx must be [B, S, C] with a contiguous last dim")
+    if ctx.dtype not in _ELEM_BYTES:
+        raise ValueError(f"context_lengths: unsupported dtype {ctx.dtype}")
+    B, S, C = ctx.shape
+    if S == 0:
+        raise ValueError("context_lengths: empty context (S = 0)")
+    seqused = torch.empty(B, dtype=torch.int32, device=ctx.device)
+    ln_pad = torch.empty(B, dtype=torch.float32, device=ctx.device)
+    ws_bytes = _lib.lib().aa_context_lengths_workspace(B, S)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=ctx.device)
+    _lib.check(
+        _lib.lib().aa_context_lengths(
+            ctx.data_ptr(), B, S, C, ctx.stride(0), ctx.stride(1), _ELEM_BYTES[ctx.dtype],
+            seqused.data_ptr(), ln_pad.data_ptr(), ws.data_ptr(), ws_bytes, _lib.stream(ctx),
+        ),
+        "context_lengths",
+    )
+    return seqused, ln_pad

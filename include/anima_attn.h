@@ -225,6 +225,32 @@ int aa_ctx_scale_bwd(const void* out, const float* lse, const float* ln_pad,
                      int64_t B, int64_t S, int64_t H, int64_t hd,
                      int dtype, void* stream);
 
+/* ------------------------------------------------------------------------ */
+/* Text-context length bookkeeping                                           */
+/* ------------------------------------------------------------------------ */
+
+/* Bytes of workspace aa_context_lengths needs (one int32 per 32 rows per item). */
+size_t aa_context_lengths_workspace(int64_t B, int64_t S);
+
+/*
+ * Lengths of a zero-padded text context ctx [B, S, C] (element strides
+ * stride_b, stride_s; last dim contiguous; elem_bytes 2 for bf16/fp16 or 4
+ * for fp32): seqused[b] = 1-based index of the last row with a non-zero
+ * element, at least 1 (int32 [B]); ln_pad[b] = log(S - seqused[b]) (float
+ * [B], -inf when nothing is padded). Computed on the device with no host
+ * read: K/V projected from the untrimmed context can go straight to
+ * aa_attn_fwd with seqused_k / ln_pad, which reads only the first seqused[b]
+ * keys, so the reference's trim to roundup8(max length) rows (and its
+ * device-to-host read) is not needed. Rows must be 16-byte aligned and
+ * C * elem_bytes a multiple of 16.
+ * Replaces: src/model.py:248-253 (the length, seqused and ln_pad lines of
+ *           encode_context's trim; the ctx[:, :keep] slice is dropped).
+ */
+int aa_context_lengths(const void* ctx, int64_t B, int64_t S, int64_t C,
+                       int64_t stride_b, int64_t stride_s, int elem_bytes,
+                       int32_t* seqused, float* ln_pad,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

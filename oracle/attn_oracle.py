@@ -200,6 +200,20 @@ def ctx_scale_backward(
     return dout, dlse
 
 
+def context_lengths(ctx: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Key lengths and log padding of a zero-padded text context (src/model.py:248-253).
+
+    length[b] = 1-based index of the last row of ctx[b] with any element != 0
+    (at least 1), seqused = length as int32, ln_pad = log(S - length) in
+    float32 (-inf when nothing is padded). -0.0 compares equal to 0; NaN does
+    not.
+    """
+    S = ctx.shape[1]
+    index = torch.arange(1, S + 1)
+    lengths = ((ctx != 0).any(-1) * index).amax(1).clamp_min(1)
+    return lengths.to(torch.int32), torch.log((S - lengths).float())
+
+
 def cross_attention_trimmed(
     q: torch.Tensor,
     k: torch.Tensor,

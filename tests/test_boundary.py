@@ -92,6 +92,9 @@ def test_workspace_sizes(lib):
     # One record per 4 tokens, then one per 16 records (the two-level reduction).
     assert lib.aa_qkv_norm_rope_bwd_workspace(1, 4096, 16, 128) == (1024 + 64) * 2 * 128 * 4
     assert lib.aa_head_norm_bwd_workspace(2, 9, 5, 128) == (5 + 1) * 128 * 4
+    # one int32 per 32 context rows per item
+    assert lib.aa_context_lengths_workspace(3, 77) == 3 * 3 * 4
+    assert lib.aa_context_lengths_workspace(0, 77) == 0
 
 
 def test_invalid_arguments_fail_before_any_launch(pkg, lib):
@@ -113,6 +116,8 @@ def test_invalid_arguments_fail_before_any_launch(pkg, lib):
     assert lib.aa_qkv_norm_rope_fwd(None, None, None, None, None, None, None, None, 1, 4, 2, 128, 1e-6, 0, None) == L.AA_EINVAL
     assert lib.aa_head_norm_fwd(None, None, None, 1, 4, 2, 96, 1e-6, 0, None) == L.AA_EUNSUPPORTED
     assert lib.aa_ctx_scale_fwd(None, None, None, None, 1, 4, 2, 128, 3, None) == L.AA_EUNSUPPORTED
+    assert lib.aa_context_lengths(None, 1, 8, 8, 64, 8, 3, None, None, None, 0, None) == L.AA_EUNSUPPORTED
+    assert lib.aa_context_lengths(None, 1, 8, 8, 64, 8, 2, None, None, None, 0, None) == L.AA_EINVAL
     with pytest.raises(ValueError):
         L.check(L.AA_EINVAL, "x")
     with pytest.raises(RuntimeError):
@@ -134,6 +139,8 @@ def test_cpu_tensors_are_rejected(pkg):
         pkg.head_norm(torch.zeros(1, 4, 128, dtype=torch.bfloat16), w, 1)
     with pytest.raises(ValueError, match="CUDA tensors required"):
         pkg.ctx_scale(q, torch.zeros(1, 1, 4), torch.zeros(1))
+    with pytest.raises(ValueError, match="CUDA tensors required"):
+        pkg.context_lengths(torch.zeros(1, 4, 8, dtype=torch.bfloat16))
     assert pkg.use_fa4(q) is False
 
 

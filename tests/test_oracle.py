@@ -287,3 +287,22 @@ def test_planted_transposed_rope_table_is_caught():
     cos, _ = ref.rope_tables(7, 5, 128)  # h and w swapped
     with pytest.raises(AssertionError):
         _close(cos, g["cos1"], atol=3e-6)
+
+
+def test_context_lengths_closed_form():
+    """Hand-built paddings: the length is the last non-zero row, whatever lies before it."""
+    ctx = torch.zeros(5, 40, 6)
+    ctx[0, :7] = 1.0  # plain padding after 7 rows
+    ctx[1, :30] = 1.0
+    ctx[1, 10:20] = 0.0  # interior zeros do not end the sequence
+    # ctx[2] all zero -> length 1
+    ctx[3, :] = 2.0  # no padding -> ln_pad = -inf
+    ctx[4, 12, 5] = -3.0  # a single non-zero element in row 12
+    ctx[4, 20:25] = -0.0  # negative zeros count as zero
+    seq, lnp = ref.context_lengths(ctx)
+    assert seq.tolist() == [7, 30, 1, 40, 13] and seq.dtype == torch.int32
+    expect = torch.tensor([math.log(33), math.log(10), math.log(39), -math.inf, math.log(27)])
+    torch.testing.assert_close(lnp, expect.float())
+    nan = torch.zeros(1, 9, 2)
+    nan[0, 6, 1] = float("nan")  # NaN is not zero
+    assert ref.context_lengths(nan)[0].tolist() == [7]
