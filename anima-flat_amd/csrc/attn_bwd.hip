@@ -13,14 +13,16 @@
 //    by role, the roles one phase apart, at the kernel); streams 64-query
 //    tiles (Q rows, dO rows, stats: 33 KB) into LDS by DMA and reads Q^T and
 //    dO^T from the same rows with transposed LDS reads. Keys are the
-//    accumulator columns (lane % 32), K and V sit in registers:
+//    accumulator columns (lane % 32), K and V sit in registers (read once
+//    from rows staged in LDS; dK and dV leave through LDS the same way):
 //      S  = Q K^T        A = Q rows (LDS),  B = K^T (registers)
 //      dP = dO V^T       A = dO rows (LDS), B = V^T (registers)
 //      dV^T += dO^T P    A = dO^T (LDS),    B = P from the S accumulators
 //      dK^T += Q^T dZ    A = Q^T (LDS),     B = dZ from the accumulators
 // 3. dq_kernel: 8 waves x 32 queries per workgroup, two groups one phase
 //    apart; streams 64-key tiles (K rows, V rows: 32 KB) and reads K^T from
-//    the K rows with transposed LDS reads. Queries are the columns:
+//    the K rows with transposed LDS reads (dQ leaves through LDS row
+//    staging). Queries are the columns:
 //      S^T = K Q^T, dP^T = V dO^T, dQ^T += K^T dZ^T.
 // The transposed reads list the keys / queries of each 16-column chunk in the
 // accumulator row order, so the bf16-rounded accumulators are the B operands
@@ -151,7 +153,8 @@ void dkdv_kernel(Params p, int nkblk, int total_blocks) {
   const int ntiles = p.ntq;
 
   // DMA by the B waves, g = wave - 4: blocks 4 g .. 4 g + 3 of the Q and dO
-  // row tiles; wave 4 also copies the stats record (kTileDma instructions).
+  // row tiles; wave 4 also copies the stats record (9 DMA instructions per
+  // tile for wave 4, 8 for the other B waves).
   const int g4 = 4 * (wave & 3);
   auto issue_tile = [&](int t) {
     const int st = t % kDkStages, q0 = t * kT, nr = min(kT, p.Sq - q0);
