@@ -257,3 +257,46 @@ def test_softmax_scale_is_inverse_sqrt_hd(pkg):
     exp = ((v[:, 0] + v[:, 1]) / 2)[:, None].expand(B, Sq, H, 128)
     parity(out, exp, max_abs=1e-2, rel_l2=4e-3, name="equal keys")
     assert math.isclose(1 / math.sqrt(128), 0.08838834764831845)
+
+
+def _random_shapes(n, seed):
+    g = torch.Generator().manual_seed(seed)
+    out = []
+    for _ in range(n):
+        B = int(torch.randint(1, 4, (1,), generator=g))
+        H = int(torch.randint(1, 6, (1,), generator=g))
+        Sq = int(torch.randint(1, 700, (1,), generator=g))
+        Sk = int(torch.randint(1, 700, (1,), generator=g))
+        out.append((B, Sq, Sk, H))
+    return out
+
+
+@pytest.mark.parametrize("B,Sq,Sk,H", _random_shapes(8, seed=2024) + [(1, 1, 1, 1), (2, 31, 1, 3)])
+def test_random_shapes_forward_backward(pkg, B, Sq, Sk, H):
+    """Seeded random sizes (partial query blocks, waves and key tiles everywhere), K and V as
+    strided views of one [B, Sk, 2, H, 128] buffer, forward and backward against the oracle."""
+    g = torch.Generator().manual_seed(B * 1000003 + Sq * 1009 + Sk * 7 + H)
+    q = ref.bf16_normal((B, Sq, H, 128), g)
+    kv = ref.bf16_normal((B, Sk, 2, H, 128), g)
+    k, v = kv[:, :, 0], kv[:, :, 1]
+    dout = ref.bf16_normal((B, Sq, H, 128), g)
+    qd = q.to("cuda", BF).requires_grad_(True)
+    kvd = kv.to("cuda", BF).requires_grad_(True)
+    out = pkg.attention(qd, kvd[:, :, 0], kvd[:, :, 1])
+    out.backward(dout.to("cuda", BF).reshape(out.shape))
+    torch.cuda.synchronize()
+    tag = f"B{B} Sq{Sq} Sk{Sk} H{H}"
+    parity(out, ref.attention_sdpa(q, k, v).reshape(B, Sq, H * 128), name=f"fwd {tag}")
+    dq, dk, dv = ref.attention_backward(q, k, v, dout)
+    if Sk == 1:
+        # One key: P = 1 and dP = D, so dQ (and dK) are exactly 0 and a relative
+        # norm is undefined; the bar is max-abs alone.
+        assert qd.grad.abs().max().item() <= 1e-5 and kvd.grad[:, :, 0].abs().max().item() <= 1e-5
+        # dV = sum of dO over all queries (P = 1): values of ~10, where one bf16
+        # rounding step alone is 2^-4; the max-abs bar is bf16's half-ulp at that size.
+        bar = max(2e-2, dv.abs().max().item() * 2.0**-8)
+        parity(kvd.grad[:, :, 1], dv, max_abs=bar, name=f"dv {tag}")
+    else:
+        parity(qd.grad, dq, name=f"dq {tag}")
+        parity(kvd.grad[:, :, 0], dk, name=f"dk {tag}")
+        parity(kvd.grad[:, :, 1], dv, name=f"dv {tag}")
