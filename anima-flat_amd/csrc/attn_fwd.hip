@@ -80,6 +80,9 @@ struct FwdParams {
   // and write normalised fp32 partials (part_o [j][split][256][128],
   // part_lse [j][split][256]) that attn_fwd_combine_kernel merges.
   int full_blocks, split_items, nsplit;
+  // Workgroups resident at once (one per CU): the unsplit blocks are mapped
+  // to work items round by round (see attn_fwd_kernel).
+  int round_blocks;
   float* part_o;
   float* part_lse;
 };
@@ -397,11 +400,18 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 
 void attn_fwd_kernel(FwdParams p) {
   __shared__ __attribute__((aligned(1024))) bf16 kv_lds[kStages][2][kTileElems];
 
-  // Block -> work item, XCD-aware over the unsplit blocks: the query blocks
-  // of one head share an XCD and its L2.
+  // Block -> work item. Blocks start in index order, so block r * R + j
+  // (R = round_blocks) runs in round r: it takes an item of that round's
+  // range [r R, r R + R), XCD-aware within the round (the query blocks of one
+  // head share an XCD and its L2). Mapping over the whole grid instead would
+  // mix items of every batch into each round, and with per-batch key lengths
+  // (seqused) every round would then last as long as the longest item.
   int item_idx, split = -1;
   if ((int)blockIdx.x < p.full_blocks) {
-    item_idx = xcd_remap(blockIdx.x, p.full_blocks);
+    const int r = (int)blockIdx.x / p.round_blocks;
+    const int j = (int)blockIdx.x - r * p.round_blocks;
+    const int in_round = min(p.round_blocks, p.full_blocks - r * p.round_blocks);
+    item_idx = r * p.round_blocks + xcd_remap(j, in_round);
   } else {
     const int j = blockIdx.x - p.full_blocks;
     item_idx = p.full_blocks + j / p.nsplit;
@@ -626,6 +636,8 @@ static int prepare(const aa_attn_fwd_args* a, FwdParams& p) {
   if (ws_need > 0 && !aligned16(a->workspace))
     return fail(AA_EINVAL, "attn_fwd: workspace must be 16-byte aligned");
   p.full_blocks = sp.full_blocks;
+  const int ncu = device_cu_count();
+  p.round_blocks = ncu > 0 ? std::min(ncu, std::max(sp.full_blocks, 1)) : std::max(sp.full_blocks, 1);
   p.split_items = sp.split_items;
   p.nsplit = sp.nsplit;
   p.part_o = (float*)a->workspace;
