@@ -54,6 +54,7 @@ _PROTOTYPES: dict[str, tuple[object, list[object]]] = {
     "aa_ctx_scale_fwd": (c_int, [c_void_p] * 4 + [_I64] * 4 + [c_int, c_void_p]),
     "aa_ctx_scale_bwd": (c_int, [c_void_p] * 6 + [_I64] * 4 + [c_int, c_void_p]),
     "aa_context_lengths_workspace": (c_size_t, [_I64] * 2),
+    "aa_rowquant": (c_int, [c_void_p, _I64, _I64, c_int, c_void_p, c_void_p, c_int, c_void_p]),
     "aa_context_lengths": (
         c_int, [c_void_p] + [_I64] * 5 + [c_int] + [c_void_p] * 3 + [c_size_t, c_void_p]
     ),

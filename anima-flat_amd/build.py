@@ -22,7 +22,10 @@ CSRC = HERE / "csrc"
 BUILD = HERE / "_build"
 LIB_NAME = "libanima_attn.so"
 LIB_PATH = HERE / LIB_NAME
-SOURCES = ("abi.hip", "prologue.hip", "ctx_scale.hip", "context.hip", "attn_fwd.hip", "attn_bwd.hip")
+SOURCES = (
+    "abi.hip", "prologue.hip", "ctx_scale.hip", "context.hip", "rowquant.hip", "attn_fwd.hip",
+    "attn_bwd.hip",
+)
 ARCH = "gfx950"
 
 # Packed fp32 VALU forms are disabled for all device code: the compiler then

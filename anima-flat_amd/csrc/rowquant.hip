@@ -1,0 +1,127 @@
+// Per-token FP8 quantisation of activations (the consumer of the attention
+// output in the FP8 model path), optionally after GELU.
+//
+// For each row x of K values: y = x (or GELU(x)), scale = max(max|y|, 1e-12)
+// / 448, q = e4m3fn(clamp(y / scale, -448, 448)) with round-to-nearest-even,
+// and the fp32 scale per row. One workgroup of 256 lanes per row, 8 values per
+// lane per chunk (K / 8 chunks spread over the lanes, K <= 8192): one HBM read
+// of the row and one write of its bytes.
+//
+// e4m3fn (OCP FP8 E4M3, "fn": no infinities, NaN = S.1111.111): exponent bias
+// 7, 3 mantissa bits, largest finite 448 = 1.75 * 2^8, normal down to 2^-6,
+// subnormals m * 2^-9. The encoding is done in integer/float arithmetic here
+// (fp8_e4m3fn_rne) so that the rounding is exactly round-to-nearest-even for
+// every input; the clamp keeps it finite.
+//
+// GELU uses the erf approximation 7.1.26 of Abramowitz and Stegun (Handbook
+// of Mathematical Functions, 1964; |error| <= 1.5e-7), the form the
+// reference's kernel uses: erf(z) ~ 1 - t (a1 + t (a2 + t (a3 + t (a4 + t a5))))
+// exp(-z^2), t = 1 / (1 + p |z|).
+#include <cmath>
+
+#include "aa_common.h"
+
+namespace aa {
+
+constexpr int kRqThreads = 256;
+constexpr int kRqMaxChunks = 4;  // chunks of 8 values per lane: K <= 8192
+
+__device__ __forceinline__ float gelu_as(float x) {
+  const float z = x * 0.7071067811865476f;
+  const float az = fabsf(z);
+  const float t = 1.0f / (1.0f + 0.3275911f * az);
+  const float poly =
+      ((((1.061405429f * t - 1.453152027f) * t + 1.421413741f) * t - 0.284496736f) * t +
+       0.254829592f) *
+      t;
+  const float y = 1.0f - poly * expf(-az * az);
+  return 0.5f * x * (1.0f + (z < 0.f ? -y : y));
+}
+
+// |v| <= 448 and finite. Round-to-nearest-even to e4m3fn.
+__device__ __forceinline__ uint32_t fp8_e4m3fn_rne(float v) {
+  const uint32_t bits = __float_as_uint(v);
+  const uint32_t sign = (bits >> 24) & 0x80u;
+  const float a = fabsf(v);
+  uint32_t code;
+  if (a < 0.015625f) {  // below 2^-6: subnormal m * 2^-9 (m = 8 is 2^-6, code 8)
+    code = (uint32_t)rintf(a * 512.0f);
+  } else {
+    const uint32_t ab = bits & 0x7fffffffu;
+    const uint32_t e = (ab >> 23) - 127u + 7u;  // biased e4m3 exponent, 1..15
+    const uint32_t mant = ab & 0x7fffffu;
+    uint32_t m3 = mant >> 20;
+    const uint32_t rem = mant & 0xfffffu;
+    if (rem > 0x80000u || (rem == 0x80000u && (m3 & 1u))) ++m3;
+    code = (e << 3) + m3;  // a carry out of the mantissa bumps the exponent
+  }
+  return sign | code;
+}
+
+__global__ __launch_bounds__(kRqThreads) void rowquant_kernel(const bf16* __restrict__ x,
+                                                              uint8_t* __restrict__ q,
+                                                              float* __restrict__ s, int K,
+                                                              int gelu) {
+  __shared__ float wave_max[kRqThreads / 64];
+  const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int nchunk = K / 8;
+  const bf16* xr = x + row * K;
+  float v[kRqMaxChunks][8];
+  float amax = 0.f;
+#pragma unroll
+  for (int c = 0; c < kRqMaxChunks; ++c) {
+    const int ch = tid + c * kRqThreads;
+    if (ch < nchunk) {
+      unpack8(ld16(xr + 8 * ch), v[c]);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        if (gelu) v[c][i] = gelu_as(v[c][i]);
+        amax = fmaxf(amax, fabsf(v[c][i]));
+      }
+    }
+  }
+  // Row max: within the wave, then over the 4 waves.
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+  if ((tid & 63) == 0) wave_max[tid >> 6] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(wave_max[0], wave_max[1]), fmaxf(wave_max[2], wave_max[3]));
+  const float scale = fmaxf(amax, 1e-12f) / 448.0f;
+  uint8_t* qr = q + row * K;
+#pragma unroll
+  for (int c = 0; c < kRqMaxChunks; ++c) {
+    const int ch = tid + c * kRqThreads;
+    if (ch < nchunk) {
+      u32x2 w = {0u, 0u};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float y = fminf(fmaxf(v[c][i] / scale, -448.0f), 448.0f);
+        w[i >> 2] |= fp8_e4m3fn_rne(y) << (8 * (i & 3));
+      }
+      *reinterpret_cast<u32x2*>(qr + 8 * ch) = w;
+    }
+  }
+  if (tid == 0) s[row] = scale;
+}
+
+}  // namespace aa
+
+using namespace aa;
+
+extern "C" int aa_rowquant(const void* x, int64_t rows, int64_t K, int gelu, void* q, float* s,
+                           int dtype, void* stream) {
+  clear_error();
+  if (dtype != AA_DTYPE_BF16) return fail(AA_EUNSUPPORTED, "rowquant: only bf16 input is implemented");
+  if (rows < 0 || K <= 0) return fail(AA_EINVAL, "rowquant: bad rows/K");
+  if (K % 8 != 0 || K > 8 * kRqThreads * kRqMaxChunks)
+    return fail(AA_EUNSUPPORTED, "rowquant: K must be a multiple of 8 and at most 8192");
+  if (rows > 0x7fffffff) return fail(AA_EUNSUPPORTED, "rowquant: too many rows");
+  if (rows == 0) return AA_OK;
+  if (!x || !q || !s) return fail(AA_EINVAL, "rowquant: null pointer");
+  if (!aligned16(x) || ((uintptr_t)q & 7u) != 0)
+    return fail(AA_EINVAL, "rowquant: x must be 16-byte and q 8-byte aligned");
+  rowquant_kernel<<<dim3((unsigned)rows), kRqThreads, 0, (hipStream_t)stream>>>(
+      (const bf16*)x, (uint8_t*)q, s, (int)K, gelu ? 1 : 0);
+  return check_launch("rowquant");
+}

@@ -287,6 +287,13 @@ def main() -> int:
             "GB/s": round(x_bytes / (us_x * 1e-3) / 1e9, 1),
             "TFLOP/s": round(x_flops / (us_x * 1e-3) / 1e12, 2),
         }
+        # FP8 row quantisation of an attention output (the model's FP8 path,
+        # rowquant(attention(...))): B=2, 4096 tokens x 2048.
+        with torch.no_grad():
+            o_att = torch.randn(2, S, H * d, generator=g).to(dev, BF)
+            us_rq = time_graph(lambda: pkg.rowquant(o_att))
+        rq_bytes = 2 * S * H * d * (2 + 1) + 2 * S * 4
+        extras["rowquant_cfg3"] = {"us": round(us_rq * 1e3, 2), "GB/s": round(rq_bytes / (us_rq * 1e-3) / 1e9, 1)}
         extras["head_norm_cfg3"] = {
             "us": round(us_hn * 1e3, 2),
             "GB/s": round(2 * 2 * S * H * d * 2 / (us_hn * 1e-3) / 1e9, 1),

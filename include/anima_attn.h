@@ -251,6 +251,22 @@ int aa_context_lengths(const void* ctx, int64_t B, int64_t S, int64_t C,
                        int32_t* seqused, float* ln_pad,
                        void* workspace, size_t workspace_bytes, void* stream);
 
+/* ------------------------------------------------------------------------ */
+/* FP8 row quantisation (consumer of the attention output)                   */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * Per-row FP8 quantisation: for each of `rows` rows of x [rows, K] bf16
+ * (contiguous), y = x or GELU(x) (gelu != 0; Abramowitz-Stegun 7.1.26 erf),
+ * s[row] = max(max|y|, 1e-12) / 448 (float), q = e4m3fn(clamp(y / s, +-448))
+ * rounded to nearest even (uint8 [rows, K], OCP E4M3 "fn" bytes).
+ * K a multiple of 8 and at most 8192; x 16-byte and q 8-byte aligned.
+ * Replaces: src/kernels/fp8.py:295-328 (rowquant, op anima_flat::rowquant),
+ *           kernel fp8.py:275-292.
+ */
+int aa_rowquant(const void* x, int64_t rows, int64_t K, int gelu,
+                void* q, float* s, int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

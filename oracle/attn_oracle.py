@@ -214,6 +214,32 @@ def context_lengths(ctx: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     return lengths.to(torch.int32), torch.log((S - lengths).float())
 
 
+def gelu_as(x: torch.Tensor) -> torch.Tensor:
+    """GELU with the Abramowitz-Stegun 7.1.26 erf approximation (src/kernels/fp8.py:260-270)."""
+    z = x * 0.7071067811865476
+    az = z.abs()
+    t = 1.0 / (1.0 + 0.3275911 * az)
+    poly = ((((1.061405429 * t - 1.453152027) * t + 1.421413741) * t - 0.284496736) * t + 0.254829592) * t
+    y = 1.0 - poly * torch.exp(-az * az)
+    return 0.5 * x * (1.0 + torch.where(z < 0, -y, y))
+
+
+def rowquant(x: torch.Tensor, gelu: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-row FP8 quantisation (src/kernels/fp8.py:275-292, op :295-310).
+
+    y = x (or GELU(x)) in float32, scale = max(max|y|, 1e-12) / 448 per row,
+    q = float8_e4m3fn(clamp(y / scale, -448, 448)) (round to nearest even).
+    Returns (q [B, S, K], scale [B*S, 1] float32).
+    """
+    B, S, K = x.shape
+    y = x.float()
+    if gelu:
+        y = gelu_as(y)
+    scale = y.abs().amax(-1, keepdim=True).clamp_min(1e-12) / 448.0
+    q = (y / scale).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
+    return q, scale.reshape(B * S, 1)
+
+
 def cross_attention_trimmed(
     q: torch.Tensor,
     k: torch.Tensor,

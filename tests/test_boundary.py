@@ -118,6 +118,9 @@ def test_invalid_arguments_fail_before_any_launch(pkg, lib):
     assert lib.aa_ctx_scale_fwd(None, None, None, None, 1, 4, 2, 128, 3, None) == L.AA_EUNSUPPORTED
     assert lib.aa_context_lengths(None, 1, 8, 8, 64, 8, 3, None, None, None, 0, None) == L.AA_EUNSUPPORTED
     assert lib.aa_context_lengths(None, 1, 8, 8, 64, 8, 2, None, None, None, 0, None) == L.AA_EINVAL
+    assert lib.aa_rowquant(None, 4, 12, 0, None, None, 0, None) == L.AA_EUNSUPPORTED  # K % 8
+    assert lib.aa_rowquant(None, 4, 16384, 0, None, None, 0, None) == L.AA_EUNSUPPORTED
+    assert lib.aa_rowquant(None, 4, 16, 0, None, None, 0, None) == L.AA_EINVAL  # null
     with pytest.raises(ValueError):
         L.check(L.AA_EINVAL, "x")
     with pytest.raises(RuntimeError):
@@ -141,12 +144,15 @@ def test_cpu_tensors_are_rejected(pkg):
         pkg.ctx_scale(q, torch.zeros(1, 1, 4), torch.zeros(1))
     with pytest.raises(ValueError, match="CUDA tensors required"):
         pkg.context_lengths(torch.zeros(1, 4, 8, dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="CUDA tensors required"):
+        pkg.rowquant(torch.zeros(1, 4, 8, dtype=torch.bfloat16))
     assert pkg.use_fa4(q) is False
 
 
 def test_ops_are_registered_with_reference_names(pkg):
     for name in ("fa_fwd", "fa_fwd_nolse", "fa_fwd_k", "fa_bwd", "qkv_norm_rope", "qkv_norm_rope_v",
-                 "qkv_norm_rope_bwd", "head_norm", "head_norm_bwd", "ctx_scale", "ctx_scale_bwd"):
+                 "qkv_norm_rope_bwd", "head_norm", "head_norm_bwd", "ctx_scale", "ctx_scale_bwd",
+                 "rowquant"):
         assert hasattr(torch.ops.anima_flat, name), name
 
 
@@ -173,6 +179,9 @@ def test_fake_shapes_on_meta_tensors(pkg):
     assert torch.ops.anima_flat.head_norm(x, w, H, 1e-6).shape == (B, Sq, H, 128)
     y = torch.ops.anima_flat.ctx_scale(q, lse, torch.empty(B, device="meta"))
     assert y.shape == q.shape
+    x = torch.empty(B, Sq, 2048, dtype=torch.bfloat16, device="meta")
+    qx, sx = torch.ops.anima_flat.rowquant(x, False)
+    assert qx.shape == x.shape and qx.dtype == torch.float8_e4m3fn and sx.shape == (B * Sq, 1)
 
 
 def test_rope_tables_bit_identical_to_oracle(pkg):

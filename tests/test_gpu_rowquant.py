@@ -1,0 +1,71 @@
+"""GPU parity of the FP8 row quantisation (aa_rowquant) against the CPU oracle.
+
+Without GELU the result is integer-exact: the same scales (float32 bits) and
+the same e4m3fn bytes as the oracle (IEEE division, round to nearest even).
+With GELU the device exp differs from the CPU's by an ulp now and then, so a
+few bytes may land on the neighbouring e4m3fn value.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import attn_oracle as ref
+
+pytestmark = pytest.mark.gpu
+
+
+def _rows(B, S, K, seed, spread=False):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(B, S, K, generator=g)
+    if spread:  # magnitudes over 2^-20 .. 2^10: many values land in the subnormal range
+        x = x * torch.exp2(torch.randint(-20, 11, (B, S, K), generator=g).float())
+    return x.to(torch.bfloat16)
+
+
+@pytest.mark.parametrize(
+    "B,S,K,spread",
+    [
+        (2, 64, 2048, False),  # attention output rows (H * hd = 2048)
+        (1, 33, 8192, False),  # MLP width, four chunks per lane
+        (3, 5, 8, False),  # one chunk per row
+        (2, 40, 2048, True),
+        (1, 7, 1000, True),  # K not a multiple of 256 * 8
+    ],
+)
+def test_rowquant_bit_exact(pkg, B, S, K, spread):
+    x = _rows(B, S, K, seed=B * 31 + S + K, spread=spread)
+    x[0, 0] = 0.0  # an all-zero row: scale 1e-12 / 448, bytes 0
+    q, s = pkg.rowquant(x.to("cuda:0"))
+    torch.cuda.synchronize()
+    eq, es = ref.rowquant(x)
+    assert q.dtype == torch.float8_e4m3fn and q.shape == x.shape and s.shape == (B * S, 1)
+    assert torch.equal(s.cpu(), es), (s.cpu() - es).abs().max()
+    qb, eb = q.cpu().view(torch.uint8), eq.view(torch.uint8)
+    assert torch.equal(qb, eb), f"{(qb != eb).sum().item()} bytes differ"
+
+
+def test_rowquant_gelu(pkg):
+    B, S, K = 2, 48, 8192
+    x = _rows(B, S, K, seed=9) * 3
+    q, s = pkg.rowquant(x.to("cuda:0"), gelu=True)
+    torch.cuda.synchronize()
+    eq, es = ref.rowquant(x, gelu=True)
+    torch.testing.assert_close(s.cpu(), es, rtol=4e-7, atol=0)
+    a, e = q.cpu().float(), eq.float()
+    diff = a != e
+    assert diff.float().mean().item() < 1e-3, diff.float().mean().item()
+    # a differing byte is the neighbouring e4m3fn value: within one e4m3 step (2^-3 relative)
+    assert ((a - e).abs() <= e.abs() * 0.1251 + 2.0**-9).all()
+
+
+def test_rowquant_of_attention_output(pkg):
+    """rowquant(attention(...)) as the model's FP8 path calls it (model.py:446)."""
+    g = torch.Generator().manual_seed(13)
+    q, k, v = (ref.bf16_normal((1, 256, 16, 128), g) for _ in range(3))
+    out = pkg.attention(*(t.to("cuda:0", torch.bfloat16) for t in (q, k, v)))
+    oq, os_ = pkg.rowquant(out)
+    torch.cuda.synchronize()
+    eq, es = ref.rowquant(out.cpu())
+    assert torch.equal(os_.cpu(), es) and torch.equal(oq.cpu().view(torch.uint8), eq.view(torch.uint8))

@@ -306,3 +306,34 @@ def test_context_lengths_closed_form():
     nan = torch.zeros(1, 9, 2)
     nan[0, 6, 1] = float("nan")  # NaN is not zero
     assert ref.context_lengths(nan)[0].tolist() == [7]
+
+
+def test_rowquant_gelu_is_the_abramowitz_stegun_erf():
+    """The GELU form is erf 7.1.26 (|error| <= 1.5e-7): against the exact erf GELU in float64."""
+    x = torch.linspace(-8, 8, 20001, dtype=torch.float64)
+    err = (ref.gelu_as(x) - F.gelu(x)).abs()
+    assert (err <= 0.5 * x.abs() * 1.6e-7 + 1e-15).all()
+    assert err.max() > 1e-9  # it is the approximation, not the exact function
+
+
+def test_rowquant_known_answers_and_closed_form():
+    # amax 448 -> scale 1: the codes are the e4m3fn round-to-nearest-even encodings.
+    row = torch.tensor([[[448.0, 1.0625, 1.1875, 2.0**-10, 1.5 * 2.0**-9, -0.0, -3.0, 0.1]]])
+    q, s = ref.rowquant(row)
+    assert s.item() == 1.0
+    # 1.0625 ties down to 1.0 (even), 1.1875 ties up to 1.25, 2^-10 ties to 0, 1.5*2^-9 to 2*2^-9
+    assert q.view(torch.uint8).flatten()[:7].tolist() == [0x7E, 0x38, 0x3A, 0x00, 0x02, 0x80, 0xC4]
+    g = torch.Generator().manual_seed(5)
+    x = (torch.randn(3, 17, 64, generator=g) * torch.logspace(-6, 3, 64)).to(torch.bfloat16)
+    x[1, 3] = 0.0  # an all-zero row
+    q, s = ref.rowquant(x)
+    xf = x.float().reshape(-1, 64)
+    amax = xf.abs().amax(-1, keepdim=True)
+    torch.testing.assert_close(s, amax.clamp_min(1e-12) / 448.0, rtol=0, atol=0)
+    deq = q.float().reshape(-1, 64) * s
+    # half an e4m3 ulp: 2^-4 relative for normals, 2^-10 * scale absolute below 2^-6 * scale
+    bound = torch.maximum(xf.abs() * 2.0**-4, s * 2.0**-10)
+    assert ((deq - xf).abs() <= bound * 1.0001).all()
+    nz = amax.squeeze(-1) > 0
+    assert (q.float().reshape(-1, 64).abs().amax(-1)[nz] == 448.0).all()
+    assert (q.reshape(-1, 64)[~nz].float() == 0).all()
