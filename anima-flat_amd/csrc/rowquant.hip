@@ -9,9 +9,13 @@
 //
 // e4m3fn (OCP FP8 E4M3, "fn": no infinities, NaN = S.1111.111): exponent bias
 // 7, 3 mantissa bits, largest finite 448 = 1.75 * 2^8, normal down to 2^-6,
-// subnormals m * 2^-9. The encoding is done in integer/float arithmetic here
-// (fp8_e4m3fn_rne) so that the rounding is exactly round-to-nearest-even for
-// every input; the clamp keeps it finite.
+// subnormals m * 2^-9. gfx950's v_cvt_pk_fp8_f32 converts to this format with
+// round-to-nearest-even: it agreed with an integer re-implementation of that
+// rounding on every fp32 value of magnitude 2^-30 .. 448 (both signs), and the
+// GPU tests check every e4m3 tie point and its fp32 neighbours through this
+// kernel. The clamp keeps the input finite and in range. (Replacing the
+// integer encoding by the instruction took the kernel from 18.8 to 12.8 us at
+// 2 x 4096 x 2048; the IEEE division is most of the rest of its VALU work.)
 //
 // GELU uses the erf approximation 7.1.26 of Abramowitz and Stegun (Handbook
 // of Mathematical Functions, 1964; |error| <= 1.5e-7), the form the
@@ -36,26 +40,6 @@ __device__ __forceinline__ float gelu_as(float x) {
       t;
   const float y = 1.0f - poly * expf(-az * az);
   return 0.5f * x * (1.0f + (z < 0.f ? -y : y));
-}
-
-// |v| <= 448 and finite. Round-to-nearest-even to e4m3fn.
-__device__ __forceinline__ uint32_t fp8_e4m3fn_rne(float v) {
-  const uint32_t bits = __float_as_uint(v);
-  const uint32_t sign = (bits >> 24) & 0x80u;
-  const float a = fabsf(v);
-  uint32_t code;
-  if (a < 0.015625f) {  // below 2^-6: subnormal m * 2^-9 (m = 8 is 2^-6, code 8)
-    code = (uint32_t)rintf(a * 512.0f);
-  } else {
-    const uint32_t ab = bits & 0x7fffffffu;
-    const uint32_t e = (ab >> 23) - 127u + 7u;  // biased e4m3 exponent, 1..15
-    const uint32_t mant = ab & 0x7fffffu;
-    uint32_t m3 = mant >> 20;
-    const uint32_t rem = mant & 0xfffffu;
-    if (rem > 0x80000u || (rem == 0x80000u && (m3 & 1u))) ++m3;
-    code = (e << 3) + m3;  // a carry out of the mantissa bumps the exponent
-  }
-  return sign | code;
 }
 
 __global__ __launch_bounds__(kRqThreads) void rowquant_kernel(const bf16* __restrict__ x,
@@ -93,11 +77,15 @@ __global__ __launch_bounds__(kRqThreads) void rowquant_kernel(const bf16* __rest
   for (int c = 0; c < kRqMaxChunks; ++c) {
     const int ch = tid + c * kRqThreads;
     if (ch < nchunk) {
-      u32x2 w = {0u, 0u};
+      float y[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float y = fminf(fmaxf(v[c][i] / scale, -448.0f), 448.0f);
-        w[i >> 2] |= fp8_e4m3fn_rne(y) << (8 * (i & 3));
+      for (int i = 0; i < 8; ++i) y[i] = fminf(fmaxf(v[c][i] / scale, -448.0f), 448.0f);
+      u32x2 w;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        int word = __builtin_amdgcn_cvt_pk_fp8_f32(y[4 * h], y[4 * h + 1], 0, false);
+        word = __builtin_amdgcn_cvt_pk_fp8_f32(y[4 * h + 2], y[4 * h + 3], word, true);
+        w[h] = (uint32_t)word;
       }
       *reinterpret_cast<u32x2*>(qr + 8 * ch) = w;
     }
@@ -112,7 +100,8 @@ using namespace aa;
 extern "C" int aa_rowquant(const void* x, int64_t rows, int64_t K, int gelu, void* q, float* s,
                            int dtype, void* stream) {
   clear_error();
-  if (dtype != AA_DTYPE_BF16) return fail(AA_EUNSUPPORTED, "rowquant: only bf16 input is implemented");
+  if (dtype != AA_DTYPE_BF16)
+    return fail(AA_EUNSUPPORTED, "rowquant: only bf16 input is implemented");
   if (rows < 0 || K <= 0) return fail(AA_EINVAL, "rowquant: bad rows/K");
   if (K % 8 != 0 || K > 8 * kRqThreads * kRqMaxChunks)
     return fail(AA_EUNSUPPORTED, "rowquant: K must be a multiple of 8 and at most 8192");

@@ -69,3 +69,30 @@ def test_rowquant_of_attention_output(pkg):
     torch.cuda.synchronize()
     eq, es = ref.rowquant(out.cpu())
     assert torch.equal(os_.cpu(), es) and torch.equal(oq.cpu().view(torch.uint8), eq.view(torch.uint8))
+
+
+def test_rowquant_every_e4m3_tie_point(pkg):
+    """Every rounding boundary of e4m3fn: each tie point between adjacent codes and its
+    neighbouring fp32 values, both signs, through the kernel with scale exactly 1 (each row
+    holds 448). Inputs are bf16, so the tie points are exact and the neighbours are the
+    adjacent bf16 values."""
+    codes = torch.arange(0, 127, dtype=torch.uint8).view(torch.float8_e4m3fn).float()
+    ties = (codes[:-1] + codes[1:]) / 2  # exact in bf16 (at most 5 significant bits)
+    tb = ties.to(torch.bfloat16)
+    assert torch.equal(tb.float(), ties)
+    up = torch.nextafter(tb, torch.tensor(1e4, dtype=torch.bfloat16))
+    down = torch.nextafter(tb, torch.tensor(0.0, dtype=torch.bfloat16))
+    vals = torch.cat([codes.to(torch.bfloat16), tb, up, down])
+    vals = torch.cat([vals, -vals])
+    K = 128
+    n = vals.numel()
+    rows = (n + K - 2) // (K - 1)
+    x = torch.zeros(rows * (K - 1), dtype=torch.bfloat16)
+    x[:n] = vals
+    x = torch.cat([torch.full((rows, 1), 448.0, dtype=torch.bfloat16), x.view(rows, K - 1)], 1)
+    x = x.view(1, rows, K)
+    q, s = pkg.rowquant(x.to("cuda:0"))
+    torch.cuda.synchronize()
+    eq, es = ref.rowquant(x)
+    assert (es == 1.0).all() and torch.equal(s.cpu(), es)
+    assert torch.equal(q.cpu().view(torch.uint8), eq.view(torch.uint8))
