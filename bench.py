@@ -179,6 +179,13 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument(
+        "--extras",
+        choices=("all", "cfg5"),
+        default="all",
+        help="which extra measurements to run after the headline: all, or only config 5's "
+        "forward + backward (a short run for profiling the backward kernels)",
+    )
+    ap.add_argument(
         "--copy-calibration",
         action="store_true",
         help="also run one plain 256 MiB device copy (known bytes) so rocprofv3 FETCH_SIZE/"
@@ -257,94 +264,95 @@ def main() -> int:
     if not args.no_extras:
         extras = {}
         steps = max(10, args.steps // 2)
-        # Prologue at config 2 (q, k written; v stays a view). The HBM-bound
-        # prologue and head_norm kernels take less GPU time than one Python op
-        # dispatch, so they are timed as HIP graphs of op calls.
-        with torch.no_grad():
-            us = time_graph(
-                lambda: pkg.qkv_norm_rope(p["qkv"], p["q_weight"], p["k_weight"], p["cos"], p["sin"], H, eps))
-        pro_bytes = 2 * B * S * H * d * 2 * 2 + 2 * S * 64 * 4  # read q,k sections; write q,k; tables
-        extras["prologue_cfg2"] = {"us": round(us * 1e3, 2), "GB/s": round(pro_bytes / (us * 1e-3) / 1e9, 1)}
-
-        # Config 3: B=2, Sq 4096, Sk 512 padded, lengths in [32,512], q-side head_norm.
-        g = torch.Generator().manual_seed(1003)
-        lens = torch.randint(32, 513, (2,), generator=g, dtype=torch.int32)
-        x = torch.randn(2, S, H * d, generator=g).to(dev, BF)
-        w = (1 + 0.02 * torch.randn(d, generator=g)).to(dev)
-        kc = torch.randn(2, 512, H, d, generator=g).to(dev, BF)
-        vc = torch.randn(2, 512, H, d, generator=g).to(dev, BF)
-        lens_d = lens.to(dev)
-        with torch.no_grad():
-            qc = pkg.head_norm(x, w, H, eps)
-            us_hn = time_graph(lambda: pkg.head_norm(x, w, H, eps))
-            _, us_x = time_launches(lambda: torch.ops.anima_flat.fa_fwd_k(qc, kc, vc, lens_d), steps, 3)
-        sl = int(lens.sum())
-        x_bytes = 2 * S * H * d * 2 * 2 + 4 * H * d * sl + 2 * H * S * 4
-        x_flops = 4.0 * H * S * d * sl
-        extras["cross_cfg3"] = {
-            "lens": lens.tolist(),
-            "us": round(us_x * 1e3, 2),
-            "GB/s": round(x_bytes / (us_x * 1e-3) / 1e9, 1),
-            "TFLOP/s": round(x_flops / (us_x * 1e-3) / 1e12, 2),
-        }
-        # FP8 row quantisation of an attention output (the model's FP8 path,
-        # rowquant(attention(...))): B=2, 4096 tokens x 2048.
-        with torch.no_grad():
-            o_att = torch.randn(2, S, H * d, generator=g).to(dev, BF)
-            us_rq = time_graph(lambda: pkg.rowquant(o_att))
-        rq_bytes = 2 * S * H * d * (2 + 1) + 2 * S * 4
-        extras["rowquant_cfg3"] = {"us": round(us_rq * 1e3, 2), "GB/s": round(rq_bytes / (us_rq * 1e-3) / 1e9, 1)}
-        extras["head_norm_cfg3"] = {
-            "us": round(us_hn * 1e3, 2),
-            "GB/s": round(2 * 2 * S * H * d * 2 / (us_hn * 1e-3) / 1e9, 1),
-        }
-
-        # Configs 1 and 4 (§8(d) table): self-attention forward % of peak and the
-        # prologue's GB/s at B=1 S=1024 (launch-latency regime), B=16 S=4096 and
-        # B=1 S=9216 (96x96 latent).
-        fwd_nolse = torch.ops.anima_flat.fa_fwd_nolse
-        for name, (Bx, Sx, seed) in (("cfg1", (1, 1024, 1001)), ("cfg4a", (16, 4096, 1004)),
-                                     ("cfg4b", (1, 9216, 1014))):
-            px = prologue_qkv(pkg, Bx, Sx, H, seed, dev)
-            nsteps = steps if Bx * Sx * Sx <= 4096 * 4096 else max(5, steps // 4)
+        if args.extras == "all":
+            # Prologue at config 2 (q, k written; v stays a view). The HBM-bound
+            # prologue and head_norm kernels take less GPU time than one Python op
+            # dispatch, so they are timed as HIP graphs of op calls.
             with torch.no_grad():
-                pro = lambda: pkg.qkv_norm_rope(px["qkv"], px["q_weight"], px["k_weight"], px["cos"],
-                                                px["sin"], H, eps)
-                qx, kx, vx = pro()
-                attn_x = lambda: fwd_nolse(qx, kx, vx)
-                prewarm(attn_x, 0.3)
-                _, us_a = time_launches(attn_x, nsteps, 3)
-                us_p = time_graph(pro, reps=20 if Bx * Sx <= 4096 else 4)
-                small = Bx * Sx <= 1024  # attention GPU time below the op's Python dispatch time
-                if small:
-                    eager_a = us_a
-                    us_a = time_graph(attn_x)
-            fl = attn_flops(Bx, H, Sx, Sx, d)
-            extras[f"self_{name}"] = {
-                "B": Bx, "seq_len": Sx, "us": round(us_a * 1e3, 2),
-                "TFLOP/s": round(fl / (us_a * 1e-3) / 1e12, 1),
-                "pct_of_peak": round(100 * fl / (us_a * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 2),
-            }
-            pb = 4 * Bx * Sx * H * d * 2 + 2 * Sx * 64 * 4  # read q,k sections; write q,k; tables
-            extras[f"prologue_{name}"] = {"us": round(us_p * 1e3, 2), "GB/s": round(pb / (us_p * 1e-3) / 1e9, 1)}
-            if small:
-                extras[f"self_{name}"]["timing"] = f"HIP graph of 20 calls; eager op {eager_a * 1e3:.1f} us"
-            del px, qx, kx, vx
-        torch.cuda.empty_cache()
+                us = time_graph(
+                    lambda: pkg.qkv_norm_rope(p["qkv"], p["q_weight"], p["k_weight"], p["cos"], p["sin"], H, eps))
+            pro_bytes = 2 * B * S * H * d * 2 * 2 + 2 * S * 64 * 4  # read q,k sections; write q,k; tables
+            extras["prologue_cfg2"] = {"us": round(us * 1e3, 2), "GB/s": round(pro_bytes / (us * 1e-3) / 1e9, 1)}
 
-        # Config 5 prologue under grad (V copied) and its backward.
-        qkv5 = p["qkv"].detach().clone().requires_grad_(True)
-        pro5 = lambda: pkg.qkv_norm_rope(qkv5, p["q_weight"], p["k_weight"], p["cos"], p["sin"], H, eps)
-        us_pf = time_graph(pro5)
-        gq, gk, gv = (torch.randn(B, S, H, d, device=dev, dtype=BF) for _ in range(3))
-        pro5_bwd = lambda: torch.ops.anima_flat.qkv_norm_rope_bwd(
-            p["qkv"], gq, gk, gv, p["q_weight"], p["k_weight"], p["cos"], p["sin"], H, eps)
-        us_pb = time_graph(pro5_bwd)
-        sec = B * S * H * d * 2  # one of q, k, v: bytes
-        extras["prologue_cfg5_fwd"] = {"us": round(us_pf * 1e3, 2),
-                                       "GB/s": round((6 * sec + 2 * S * 64 * 4) / (us_pf * 1e-3) / 1e9, 1)}
-        extras["prologue_cfg5_bwd"] = {"us": round(us_pb * 1e3, 2),
-                                       "GB/s": round((9 * sec + 2 * S * 64 * 4) / (us_pb * 1e-3) / 1e9, 1)}
+            # Config 3: B=2, Sq 4096, Sk 512 padded, lengths in [32,512], q-side head_norm.
+            g = torch.Generator().manual_seed(1003)
+            lens = torch.randint(32, 513, (2,), generator=g, dtype=torch.int32)
+            x = torch.randn(2, S, H * d, generator=g).to(dev, BF)
+            w = (1 + 0.02 * torch.randn(d, generator=g)).to(dev)
+            kc = torch.randn(2, 512, H, d, generator=g).to(dev, BF)
+            vc = torch.randn(2, 512, H, d, generator=g).to(dev, BF)
+            lens_d = lens.to(dev)
+            with torch.no_grad():
+                qc = pkg.head_norm(x, w, H, eps)
+                us_hn = time_graph(lambda: pkg.head_norm(x, w, H, eps))
+                _, us_x = time_launches(lambda: torch.ops.anima_flat.fa_fwd_k(qc, kc, vc, lens_d), steps, 3)
+            sl = int(lens.sum())
+            x_bytes = 2 * S * H * d * 2 * 2 + 4 * H * d * sl + 2 * H * S * 4
+            x_flops = 4.0 * H * S * d * sl
+            extras["cross_cfg3"] = {
+                "lens": lens.tolist(),
+                "us": round(us_x * 1e3, 2),
+                "GB/s": round(x_bytes / (us_x * 1e-3) / 1e9, 1),
+                "TFLOP/s": round(x_flops / (us_x * 1e-3) / 1e12, 2),
+            }
+            # FP8 row quantisation of an attention output (the model's FP8 path,
+            # rowquant(attention(...))): B=2, 4096 tokens x 2048.
+            with torch.no_grad():
+                o_att = torch.randn(2, S, H * d, generator=g).to(dev, BF)
+                us_rq = time_graph(lambda: pkg.rowquant(o_att))
+            rq_bytes = 2 * S * H * d * (2 + 1) + 2 * S * 4
+            extras["rowquant_cfg3"] = {"us": round(us_rq * 1e3, 2), "GB/s": round(rq_bytes / (us_rq * 1e-3) / 1e9, 1)}
+            extras["head_norm_cfg3"] = {
+                "us": round(us_hn * 1e3, 2),
+                "GB/s": round(2 * 2 * S * H * d * 2 / (us_hn * 1e-3) / 1e9, 1),
+            }
+
+            # Configs 1 and 4 (§8(d) table): self-attention forward % of peak and the
+            # prologue's GB/s at B=1 S=1024 (launch-latency regime), B=16 S=4096 and
+            # B=1 S=9216 (96x96 latent).
+            fwd_nolse = torch.ops.anima_flat.fa_fwd_nolse
+            for name, (Bx, Sx, seed) in (("cfg1", (1, 1024, 1001)), ("cfg4a", (16, 4096, 1004)),
+                                         ("cfg4b", (1, 9216, 1014))):
+                px = prologue_qkv(pkg, Bx, Sx, H, seed, dev)
+                nsteps = steps if Bx * Sx * Sx <= 4096 * 4096 else max(5, steps // 4)
+                with torch.no_grad():
+                    pro = lambda: pkg.qkv_norm_rope(px["qkv"], px["q_weight"], px["k_weight"], px["cos"],
+                                                    px["sin"], H, eps)
+                    qx, kx, vx = pro()
+                    attn_x = lambda: fwd_nolse(qx, kx, vx)
+                    prewarm(attn_x, 0.3)
+                    _, us_a = time_launches(attn_x, nsteps, 3)
+                    us_p = time_graph(pro, reps=20 if Bx * Sx <= 4096 else 4)
+                    small = Bx * Sx <= 1024  # attention GPU time below the op's Python dispatch time
+                    if small:
+                        eager_a = us_a
+                        us_a = time_graph(attn_x)
+                fl = attn_flops(Bx, H, Sx, Sx, d)
+                extras[f"self_{name}"] = {
+                    "B": Bx, "seq_len": Sx, "us": round(us_a * 1e3, 2),
+                    "TFLOP/s": round(fl / (us_a * 1e-3) / 1e12, 1),
+                    "pct_of_peak": round(100 * fl / (us_a * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 2),
+                }
+                pb = 4 * Bx * Sx * H * d * 2 + 2 * Sx * 64 * 4  # read q,k sections; write q,k; tables
+                extras[f"prologue_{name}"] = {"us": round(us_p * 1e3, 2), "GB/s": round(pb / (us_p * 1e-3) / 1e9, 1)}
+                if small:
+                    extras[f"self_{name}"]["timing"] = f"HIP graph of 20 calls; eager op {eager_a * 1e3:.1f} us"
+                del px, qx, kx, vx
+            torch.cuda.empty_cache()
+
+            # Config 5 prologue under grad (V copied) and its backward.
+            qkv5 = p["qkv"].detach().clone().requires_grad_(True)
+            pro5 = lambda: pkg.qkv_norm_rope(qkv5, p["q_weight"], p["k_weight"], p["cos"], p["sin"], H, eps)
+            us_pf = time_graph(pro5)
+            gq, gk, gv = (torch.randn(B, S, H, d, device=dev, dtype=BF) for _ in range(3))
+            pro5_bwd = lambda: torch.ops.anima_flat.qkv_norm_rope_bwd(
+                p["qkv"], gq, gk, gv, p["q_weight"], p["k_weight"], p["cos"], p["sin"], H, eps)
+            us_pb = time_graph(pro5_bwd)
+            sec = B * S * H * d * 2  # one of q, k, v: bytes
+            extras["prologue_cfg5_fwd"] = {"us": round(us_pf * 1e3, 2),
+                                           "GB/s": round((6 * sec + 2 * S * 64 * 4) / (us_pf * 1e-3) / 1e9, 1)}
+            extras["prologue_cfg5_bwd"] = {"us": round(us_pb * 1e3, 2),
+                                           "GB/s": round((9 * sec + 2 * S * 64 * 4) / (us_pb * 1e-3) / 1e9, 1)}
 
         # Config 5: forward + backward (LoRA training attention), B=1, 4096.
         qg, kg, vg = (t.detach().clone().requires_grad_(True) for t in (q, k, v.contiguous()))
@@ -365,73 +373,75 @@ def main() -> int:
             "pct_of_peak": round(100 * fb_flops / (us_fb * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 2),
         }
 
-        # One CFG denoiser step at 1024x1024: 28 layers x (prologue + self-attn B=2 S=4096
-        # + head_norm + cross-attn over 512 untrimmed keys).
-        p2 = prologue_qkv(pkg, 2, S, H, 1010, dev)
-        x2 = torch.randn(2, S, H * d, device=dev, dtype=BF)
-        k2 = torch.randn(2, 512, H, d, device=dev, dtype=BF)
-        v2 = torch.randn(2, 512, H, d, device=dev, dtype=BF)
+        if args.extras == "all":
+            # One CFG denoiser step at 1024x1024: 28 layers x (prologue + self-attn B=2 S=4096
+            # + head_norm + cross-attn over 512 untrimmed keys).
+            p2 = prologue_qkv(pkg, 2, S, H, 1010, dev)
+            x2 = torch.randn(2, S, H * d, device=dev, dtype=BF)
+            k2 = torch.randn(2, 512, H, d, device=dev, dtype=BF)
+            v2 = torch.randn(2, 512, H, d, device=dev, dtype=BF)
 
-        def layer():
-            qq, kk, vv = pkg.qkv_norm_rope(p2["qkv"], p2["q_weight"], p2["k_weight"], p2["cos"], p2["sin"], H, eps)
-            pkg.attention(qq, kk, vv)
-            qx = pkg.head_norm(x2, w, H, eps)
-            pkg.attention(qx, k2, v2)
+            def layer():
+                qq, kk, vv = pkg.qkv_norm_rope(p2["qkv"], p2["q_weight"], p2["k_weight"], p2["cos"], p2["sin"], H, eps)
+                pkg.attention(qq, kk, vv)
+                qx = pkg.head_norm(x2, w, H, eps)
+                pkg.attention(qx, k2, v2)
 
-        with torch.no_grad():
-            _, us_layer = time_launches(layer, 28, 3)
-        extras["denoiser_step_attn_ms"] = {
-            "ms": round(28 * us_layer, 3),
-            "per_layer_us": round(us_layer * 1e3, 1),
-            "what": "28 x (qkv_norm_rope + self-attn B2 S4096 + head_norm + cross-attn B2 Sk512 untrimmed)",
-            "reference_h100_nvl_ms": 20.13,
-        }
-        # The reference's 20.13 ms is its 56 attention kernel calls alone (28 self + 28
-        # cross): the same two calls here, without the prologue and head_norm.
-        qq2, kk2, vv2 = pkg.qkv_norm_rope(p2["qkv"], p2["q_weight"], p2["k_weight"], p2["cos"],
-                                          p2["sin"], H, eps)
-        qx2 = pkg.head_norm(x2, w, H, eps)
+            with torch.no_grad():
+                _, us_layer = time_launches(layer, 28, 3)
+            extras["denoiser_step_attn_ms"] = {
+                "ms": round(28 * us_layer, 3),
+                "per_layer_us": round(us_layer * 1e3, 1),
+                "what": "28 x (qkv_norm_rope + self-attn B2 S4096 + head_norm + cross-attn B2 Sk512 untrimmed)",
+                "reference_h100_nvl_ms": 20.13,
+            }
+            # The reference's 20.13 ms is its 56 attention kernel calls alone (28 self + 28
+            # cross): the same two calls here, without the prologue and head_norm.
+            qq2, kk2, vv2 = pkg.qkv_norm_rope(p2["qkv"], p2["q_weight"], p2["k_weight"], p2["cos"],
+                                              p2["sin"], H, eps)
+            qx2 = pkg.head_norm(x2, w, H, eps)
 
-        def attn_calls():
-            pkg.attention(qq2, kk2, vv2)
-            pkg.attention(qx2, k2, v2)
+            def attn_calls():
+                pkg.attention(qq2, kk2, vv2)
+                pkg.attention(qx2, k2, v2)
 
-        with torch.no_grad():
-            _, us_calls = time_launches(attn_calls, 28, 3)
-        extras["denoiser_step_attn_calls_ms"] = {
-            "ms": round(28 * us_calls, 3),
-            "what": "28 x (self-attn B2 S4096 + cross-attn B2 Sk512 untrimmed): the 56 calls the "
-                    "reference figure counts",
-            "reference_h100_nvl_ms": 20.13,
-        }
-        # With the text context trimmed (the reference's --trim-context mode): key lengths of
-        # a zero-padded context (config 3's lengths) computed on the device once per prompt,
-        # then masked cross-attention with the fused padding correction on the untrimmed K/V.
-        ctx = torch.zeros(2, 512, 1024, device=dev, dtype=BF)
-        for b, n in enumerate(lens.tolist()):
-            ctx[b, :n] = torch.randn(n, 1024, device=dev, dtype=BF)
-            ctx[b, n - 1, 0] = 1.0
-        seq2, lnp2 = pkg.context_lengths(ctx)
+            with torch.no_grad():
+                _, us_calls = time_launches(attn_calls, 28, 3)
+            extras["denoiser_step_attn_calls_ms"] = {
+                "ms": round(28 * us_calls, 3),
+                "what": "28 x (self-attn B2 S4096 + cross-attn B2 Sk512 untrimmed): the 56 calls the "
+                        "reference figure counts",
+                "reference_h100_nvl_ms": 20.13,
+            }
+            # With the text context trimmed (the reference's --trim-context mode): key lengths of
+            # a zero-padded context (config 3's lengths) computed on the device once per prompt,
+            # then masked cross-attention with the fused padding correction on the untrimmed K/V.
+            ctx = torch.zeros(2, 512, 1024, device=dev, dtype=BF)
+            for b, n in enumerate(lens.tolist()):
+                ctx[b, :n] = torch.randn(n, 1024, device=dev, dtype=BF)
+                ctx[b, n - 1, 0] = 1.0
+            seq2, lnp2 = pkg.context_lengths(ctx)
 
-        def layer_trim():
-            qq, kk, vv = pkg.qkv_norm_rope(p2["qkv"], p2["q_weight"], p2["k_weight"], p2["cos"], p2["sin"], H, eps)
-            pkg.attention(qq, kk, vv)
-            qx = pkg.head_norm(x2, w, H, eps)
-            pkg.cross_attention_trimmed(qx, k2, v2, seq2, lnp2)
+            def layer_trim():
+                qq, kk, vv = pkg.qkv_norm_rope(p2["qkv"], p2["q_weight"], p2["k_weight"], p2["cos"], p2["sin"], H, eps)
+                pkg.attention(qq, kk, vv)
+                qx = pkg.head_norm(x2, w, H, eps)
+                pkg.cross_attention_trimmed(qx, k2, v2, seq2, lnp2)
 
-        with torch.no_grad():
-            _, us_trim = time_launches(layer_trim, 28, 3)
-            us_lens = time_graph(lambda: pkg.context_lengths(ctx))
-        extras["denoiser_step_attn_ms_trimmed_ctx"] = {
-            "ms": round(28 * us_trim, 3),
-            "per_layer_us": round(us_trim * 1e3, 1),
-            "lens": seq2.tolist(),
-            "context_lengths_us": round(us_lens * 1e3, 2),
-            "what": "as denoiser_step_attn_ms, cross-attn over the first seqused keys with the fused "
-                    "padding correction (lengths from context_lengths, once per prompt)",
-        }
+            with torch.no_grad():
+                _, us_trim = time_launches(layer_trim, 28, 3)
+                us_lens = time_graph(lambda: pkg.context_lengths(ctx))
+            extras["denoiser_step_attn_ms_trimmed_ctx"] = {
+                "ms": round(28 * us_trim, 3),
+                "per_layer_us": round(us_trim * 1e3, 1),
+                "lens": seq2.tolist(),
+                "context_lengths_us": round(us_lens * 1e3, 2),
+                "what": "as denoiser_step_attn_ms, cross-attn over the first seqused keys with the fused "
+                        "padding correction (lengths from context_lengths, once per prompt)",
+            }
         result["extras"] = extras
-        result["per_step_attn_ms"] = extras["denoiser_step_attn_ms"]["ms"]
+        if "denoiser_step_attn_ms" in extras:
+            result["per_step_attn_ms"] = extras["denoiser_step_attn_ms"]["ms"]
 
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline()
