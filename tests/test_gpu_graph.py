@@ -1,0 +1,63 @@
+"""The path's launches under HIP-graph capture: replays equal the eager results.
+
+bench.py times the short ops as HIP graphs, and a caller may capture the
+denoiser step. Every entry point launches only kernels (no memsets, no host
+reads, workspaces from the caller), so a captured sequence must reproduce the
+eager outputs bit for bit on every replay, with other eager work in between.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import attn_oracle as ref
+
+pytestmark = pytest.mark.gpu
+
+BF = torch.bfloat16
+
+
+def test_graph_replays_match_eager(pkg):
+    dev = torch.device("cuda:0")
+    B, S, H, d = 2, 512, 4, 128
+    inp = ref.prologue_inputs(B, S, H, d, seed=77)
+    qkv = inp["qkv"].to(dev, BF)
+    qw, kw = inp["q_weight"].to(dev), inp["k_weight"].to(dev)
+    cos, sin = inp["cos"].to(dev), inp["sin"].to(dev)
+    g = torch.Generator().manual_seed(78)
+    x = ref.bf16_normal((B, 300, H * d), g).to(dev, BF)
+    w = ref.norm_weight(d, g).to(dev)
+    kc = ref.bf16_normal((B, 96, H, d), g).to(dev, BF)
+    vc = ref.bf16_normal((B, 96, H, d), g).to(dev, BF)
+    ctx = torch.zeros(B, 96, 64, dtype=BF, device=dev)
+    ctx[0, :40] = 1.0
+    ctx[1, :71] = -2.0
+
+    def step():
+        q, k, v = pkg.qkv_norm_rope(qkv, qw, kw, cos, sin, H, 1e-6)
+        o_self = pkg.attention(q, k, v)
+        qx = pkg.head_norm(x, w, H, 1e-6)
+        seq, lnp = pkg.context_lengths(ctx)
+        o_cross = pkg.cross_attention_trimmed(qx, kc, vc, seq, lnp)
+        oq, os_ = pkg.rowquant(o_self)
+        return [o_self, o_cross, oq.view(torch.uint8), os_, seq, lnp]
+
+    with torch.no_grad():
+        eager = [t.clone() for t in step()]
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            step()  # warm the caching allocator on the capture stream
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            outs = step()
+        for i in range(3):
+            # eager work in between that reuses the same kernels on other data
+            pkg.attention(*(ref.bf16_normal((1, 130, 2, d), g).to(dev, BF) for _ in range(3)))
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            for a, e in zip(outs, eager):
+                assert torch.equal(a, e), f"replay {i}: {a.dtype} {tuple(a.shape)} differs"
