@@ -147,12 +147,18 @@ struct KVDma {
                                         int t, bf16* kd, bf16* vd) const {
     const int kb = t * kBN;
     if (kb + kBN <= klen) {
+      // Chunks lq + 4 i of one row: 64-byte steps, as immediate offsets.
+      static_assert(kDmaPerWave == 4, "four DMA blocks per wave per tile");
       const bf16* vt = vp + (int64_t)kb * p.vs1 + voff;
-#pragma unroll
-      for (int i = 0; i < kDmaPerWave; ++i) dma16(vt + 32 * i, vd + (b0 + i) * 512);
+      dma16_off<0>(vt, vd + b0 * 512);
+      dma16_off<64>(vt, vd + (b0 + 1) * 512);
+      dma16_off<128>(vt, vd + (b0 + 2) * 512);
+      dma16_off<192>(vt, vd + (b0 + 3) * 512);
       const bf16* kt = kp + (int64_t)kb * p.ks1 + koff;
-#pragma unroll
-      for (int i = 0; i < kDmaPerWave; ++i) dma16(kt + 32 * i, kd + (b0 + i) * 512);
+      dma16_off<0>(kt, kd + b0 * 512);
+      dma16_off<64>(kt, kd + (b0 + 1) * 512);
+      dma16_off<128>(kt, kd + (b0 + 2) * 512);
+      dma16_off<192>(kt, kd + (b0 + 3) * 512);
     } else {
       const int vr = min(kb + vrow, klen - 1);
       const int kr = min(kb + krow, klen - 1);

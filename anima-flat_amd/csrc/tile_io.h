@@ -78,6 +78,21 @@ __device__ __forceinline__ void dma16(const void* src, const void* lds_base) {
                : "memory", "m0");
 }
 
+// The same with a compile-time byte offset on the global address
+// (global_load_lds_dwordx4's immediate offset, 0 <= kOff < 4096): DMAs from
+// one base at fixed strides share one address computation. The instruction
+// adds its offset to the LDS address as well (M0 + offset + 16 * lane), so M0
+// is set kOff bytes below the destination.
+template <int kOff>
+__device__ __forceinline__ void dma16_off(const void* src, const void* lds_base) {
+  static_assert(kOff >= 0 && kOff < 4096, "immediate offset range");
+  const uint32_t m0 =
+      __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void*)lds_base) - (uint32_t)kOff;
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off offset:%2" ::"v"(src), "s"(m0),
+               "n"(kOff)
+               : "memory", "m0");
+}
+
 __device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // One DMA block (blk in 0..15) of a swizzled row tile whose row 0 is at
