@@ -155,15 +155,11 @@ void dkdv_kernel(Params p, int nkblk, int total_blocks) {
   // DMA by the B waves, g = wave - 4: blocks 4 g .. 4 g + 3 of the Q and dO
   // row tiles; wave 4 also copies the stats record (9 DMA instructions per
   // tile for wave 4, 8 for the other B waves).
-  const int g4 = 4 * (wave & 3);
+  const int g = wave & 3;
   auto issue_tile = [&](int t) {
     const int st = t % kDkStages, q0 = t * kT, nr = min(kT, p.Sq - q0);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      dma_row_block_swz(qbase + (int64_t)q0 * p.s_q[1], p.s_q[1], nr, rows[st][0], g4 + i, lane);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      dma_row_block_swz(dobase + (int64_t)q0 * p.s_do[1], p.s_do[1], nr, rows[st][1], g4 + i, lane);
+    dma_row_quad_swz(qbase + (int64_t)q0 * p.s_q[1], p.s_q[1], nr, rows[st][0], g, lane);
+    dma_row_quad_swz(dobase + (int64_t)q0 * p.s_do[1], p.s_do[1], nr, rows[st][1], g, lane);
     if (wave == 4) dma16(statb + (int64_t)t * kStat + 4 * lane, stat[st]);
   };
 
@@ -373,15 +369,11 @@ void dq_kernel(Params p, int nqblk, int total_blocks) {
   const int ntiles = p.ntk;
 
   // DMA by group A, g = wave: blocks 4 g .. 4 g + 3 of the K and V row tiles.
-  const int g4 = 4 * (wave & 3);
+  const int g = wave & 3;
   auto issue_tile = [&](int t) {
     const int st = t % kDqStages, k0 = t * kT, nr = min(kT, p.Sk - k0);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      dma_row_block_swz(kbase + (int64_t)k0 * p.s_k[1], p.s_k[1], nr, tiles[st][0], g4 + i, lane);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      dma_row_block_swz(vbase + (int64_t)k0 * p.s_v[1], p.s_v[1], nr, tiles[st][1], g4 + i, lane);
+    dma_row_quad_swz(kbase + (int64_t)k0 * p.s_k[1], p.s_k[1], nr, tiles[st][0], g, lane);
+    dma_row_quad_swz(vbase + (int64_t)k0 * p.s_v[1], p.s_v[1], nr, tiles[st][1], g, lane);
   };
 
   // Read offsets in the swizzled row tiles (tile_io.h): row operands (row

@@ -95,15 +95,20 @@ __device__ __forceinline__ void dma16_off(const void* src, const void* lds_base)
 
 __device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-// One DMA block (blk in 0..15) of a swizzled row tile whose row 0 is at
-// `base` (row stride rs elements): rows 16 (blk >> 2) + ((lane & 15) ^
-// (4 (lane >> 4))), chunk 4 (blk & 3) + (lane >> 4). Rows at or past `nrows`
-// (>= 1) re-read row nrows - 1, finite data the caller masks.
-__device__ __forceinline__ void dma_row_block_swz(const bf16* base, int64_t rs, int nrows,
-                                                  const bf16* lds_tile, int blk, int lane) {
-  const int row = min(16 * (blk >> 2) + ((lane & 15) ^ (4 * (lane >> 4))), nrows - 1);
-  const int chunk = 4 * (blk & 3) + (lane >> 4);
-  dma16(base + (int64_t)row * rs + 8 * chunk, lds_tile + blk * 512);
+// DMA blocks 4 g .. 4 g + 3 of a swizzled row tile whose row 0 is at `base`
+// (row stride rs elements): rows 16 g + ((lane & 15) ^ (4 lq)), lq = lane >> 4,
+// chunk 4 i + lq for block 4 g + i. The four blocks read the same rows, so
+// they share one address with immediate offsets of 64 i bytes. Rows at or
+// past `nrows` (>= 1) re-read row nrows - 1, finite data the caller masks.
+__device__ __forceinline__ void dma_row_quad_swz(const bf16* base, int64_t rs, int nrows,
+                                                 const bf16* lds_tile, int g, int lane) {
+  const int row = min(16 * g + ((lane & 15) ^ (4 * (lane >> 4))), nrows - 1);
+  const bf16* src = base + (int64_t)row * rs + 8 * (lane >> 4);
+  const bf16* dst = lds_tile + 4 * g * 512;
+  dma16_off<0>(src, dst);
+  dma16_off<64>(src, dst + 512);
+  dma16_off<128>(src, dst + 1024);
+  dma16_off<192>(src, dst + 1536);
 }
 
 // Transposed operand reads ---------------------------------------------------
