@@ -444,15 +444,21 @@ void dq_kernel(Params p, int nqblk, int total_blocks) {
   auto xblock = [&](int t) {
     if (group_a && t + 2 < ntiles) issue_tile(t + 2);
     const int kb = t * kT;
-    const bool partial = kb + kT > p.Sk;
+    // Keys past Sk (last tile only, a wave-uniform branch) get S = -inf, so
+    // P = 0. Masking per element on every tile, as a select after the exp,
+    // put ~96 VALU instructions into every softmax phase.
+    if (kb + kT > p.Sk) {
+#pragma unroll
+      for (int hk = 0; hk < 2; ++hk)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (kb + 32 * hk + 8 * (r >> 2) + 4 * hh + (r & 3) >= p.Sk) s[hk][r] = -INFINITY;
+    }
 #pragma unroll
     for (int hk = 0; hk < 2; ++hk)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float pv = fast_exp2(fmaf(s[hk][r], c, -lse2));
-        if (partial && kb + 32 * hk + 8 * (r >> 2) + 4 * hh + (r & 3) >= p.Sk) pv = 0.f;
-        zb[2 * hk + (r >> 3)][r & 7] = (bf16)(pv * dp[hk][r]);
-      }
+      for (int r = 0; r < 16; ++r)
+        zb[2 * hk + (r >> 3)][r & 7] = (bf16)(fast_exp2(fmaf(s[hk][r], c, -lse2)) * dp[hk][r]);
     // The wait takes the dZ operands as inputs so that it stays after the
     // VALU work above (a plain asm statement may be hoisted over it).
     if (group_a) {
