@@ -59,6 +59,21 @@ __device__ __forceinline__ u32x4 pack8(const float* f) {
   return w;
 }
 
+// max(a, b, c) in one v_max3_f32 and max(a, b) in one v_max_f32. fmaxf would
+// first canonicalise its inputs (IEEE NaN quieting, an extra v_max_f32 each);
+// the path's scores hold no NaN.
+__device__ __forceinline__ float max3f(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
+__device__ __forceinline__ float max2f(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+
 // Reductions over the lane pair (l, l ^ 32) with v_permlane32_swap_b32. The
 // instruction swaps lanes 32-63 of its first operand with lanes 0-31 of its
 // second; with x in both, every lane ends up holding {own, partner} across
@@ -66,7 +81,7 @@ __device__ __forceinline__ u32x4 pack8(const float* f) {
 // gives the pair reduction in all 64 lanes.
 __device__ __forceinline__ float pair_max(float x) {
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  return max2f(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
 __device__ __forceinline__ float pair_sum(float x) {
@@ -75,14 +90,6 @@ __device__ __forceinline__ float pair_sum(float x) {
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
-
-// max(a, b, c) in one v_max3_f32. fmaxf would first canonicalise its inputs
-// (IEEE NaN quieting, an extra v_max_f32 each); the path's scores hold no NaN.
-__device__ __forceinline__ float max3f(float a, float b, float c) {
-  float r;
-  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
-  return r;
-}
 
 // Sum over aligned groups of `width` lanes (width a power of two <= 64).
 template <int WIDTH>

@@ -287,7 +287,7 @@ struct FwdWave {
       ma = max3f(ma, s0[r], s1[r]);
       mb = max3f(mb, s0[r + 1], s1[r + 1]);
     }
-    float mt = max3f(ma, mb, fmaxf(s0[15], s1[15]));
+    float mt = max3f(ma, mb, max2f(s0[15], s1[15]));
     mt = pair_max(mt);
 
     const bool need = mt > m_raw + thr_raw;
