@@ -42,6 +42,47 @@ __device__ __forceinline__ float gelu_as(float x) {
   return 0.5f * x * (1.0f + (z < 0.f ? -y : y));
 }
 
+// Quantise this lane's chunks of the row: y / scale (correctly rounded),
+// clamp, e4m3fn. With kMarkstein the quotient comes from the correctly
+// rounded reciprocal rcp of the scale (Markstein): q0 = RN(y * rcp) is within
+// an ulp of the quotient, e = y - q0 * scale is exact (FMA), and
+// RN(q0 + e * rcp) is the correctly rounded quotient unless something
+// underflows. The caller takes this path when the row's amax is at least
+// 2^-60: a quotient whose remainder could underflow is then below 2^-60
+// itself and encodes to zero either way. Other rows divide.
+template <bool kMarkstein>
+__device__ __forceinline__ void rq_store(const float (&v)[kRqMaxChunks][8], float scale, float rcp,
+                                         int nchunk, int tid, uint8_t* qr) {
+#pragma unroll
+  for (int c = 0; c < kRqMaxChunks; ++c) {
+    const int ch = tid + c * kRqThreads;
+    if (ch < nchunk) {
+      float y[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float t;
+        if constexpr (kMarkstein) {
+          // The sign is the input's (scale > 0); the FMAs alone would turn
+          // -0.0 into +0.0 (-0 + +0 rounds to +0), which the division keeps.
+          const float q0 = v[c][i] * rcp;
+          t = copysignf(fmaf(fmaf(-q0, scale, v[c][i]), rcp, q0), v[c][i]);
+        } else {
+          t = v[c][i] / scale;
+        }
+        y[i] = fminf(fmaxf(t, -448.0f), 448.0f);
+      }
+      u32x2 w;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        int word = __builtin_amdgcn_cvt_pk_fp8_f32(y[4 * h], y[4 * h + 1], 0, false);
+        word = __builtin_amdgcn_cvt_pk_fp8_f32(y[4 * h + 2], y[4 * h + 3], word, true);
+        w[h] = (uint32_t)word;
+      }
+      *reinterpret_cast<u32x2*>(qr + 8 * ch) = w;
+    }
+  }
+}
+
 __global__ __launch_bounds__(kRqThreads) void rowquant_kernel(const bf16* __restrict__ x,
                                                               uint8_t* __restrict__ q,
                                                               float* __restrict__ s, int K,
@@ -73,22 +114,10 @@ __global__ __launch_bounds__(kRqThreads) void rowquant_kernel(const bf16* __rest
   amax = fmaxf(fmaxf(wave_max[0], wave_max[1]), fmaxf(wave_max[2], wave_max[3]));
   const float scale = fmaxf(amax, 1e-12f) / 448.0f;
   uint8_t* qr = q + row * K;
-#pragma unroll
-  for (int c = 0; c < kRqMaxChunks; ++c) {
-    const int ch = tid + c * kRqThreads;
-    if (ch < nchunk) {
-      float y[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) y[i] = fminf(fmaxf(v[c][i] / scale, -448.0f), 448.0f);
-      u32x2 w;
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        int word = __builtin_amdgcn_cvt_pk_fp8_f32(y[4 * h], y[4 * h + 1], 0, false);
-        word = __builtin_amdgcn_cvt_pk_fp8_f32(y[4 * h + 2], y[4 * h + 3], word, true);
-        w[h] = (uint32_t)word;
-      }
-      *reinterpret_cast<u32x2*>(qr + 8 * ch) = w;
-    }
+  if (amax >= 0x1p-60f) {
+    rq_store<true>(v, scale, 1.0f / scale, nchunk, tid, qr);
+  } else {
+    rq_store<false>(v, scale, 0.f, nchunk, tid, qr);
   }
   if (tid == 0) s[row] = scale;
 }
