@@ -15,7 +15,7 @@
 // GPU tests check every e4m3 tie point and its fp32 neighbours through this
 // kernel. The clamp keeps the input finite and in range. (Replacing the
 // integer encoding by the instruction took the kernel from 18.8 to 12.8 us at
-// 2 x 4096 x 2048; the IEEE division is most of the rest of its VALU work.)
+// 2 x 4096 x 2048, the reciprocal-based quotients in rq_store to 11.8 us.)
 //
 // GELU uses the erf approximation 7.1.26 of Abramowitz and Stegun (Handbook
 // of Mathematical Functions, 1964; |error| <= 1.5e-7), the form the
