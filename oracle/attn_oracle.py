@@ -263,6 +263,56 @@ def attention_backward(
     return qq.grad, kk.grad, vv.grad
 
 
+def attention_backward_rows(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    dout: torch.Tensor,
+    qrows: torch.Tensor,
+    krows: torch.Tensor,
+    chunk: int = 1024,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """(dq[:, qrows], dk[:, krows], dv[:, krows]) of `attention_sdpa` for long
+    sequences, from the closed-form softmax gradient (what FA4's backward,
+    src/attention.py:91-103, computes), without the full [Sq, Sk] matrix:
+
+        P = softmax(s), s = q k^T / sqrt(hd), D_i = dO_i . O_i,
+        dS_ij = P_ij (dO_i . v_j - D_i),
+        dq_i = sum_j dS_ij k_j / sqrt(hd), dk_j = sum_i dS_ij q_i / sqrt(hd),
+        dv_j = sum_i P_ij dO_i.
+
+    Query rows are processed `chunk` at a time. Float32 throughout.
+    """
+    q, k, v, dout = (t.float() for t in (q, k, v, dout))
+    scale = 1.0 / math.sqrt(q.shape[-1])
+    kr, vr = k[:, krows], v[:, krows]
+    dk = torch.zeros_like(kr)
+    dv = torch.zeros_like(vr)
+    qsel = torch.zeros(q.shape[1], dtype=torch.bool)
+    qsel[qrows] = True
+    dq = torch.zeros_like(q[:, qrows])
+    done = 0
+    for c0 in range(0, q.shape[1], chunk):
+        qc, doc = q[:, c0 : c0 + chunk], dout[:, c0 : c0 + chunk]
+        s = torch.einsum("bqhd,bkhd->bhqk", qc, k) * scale
+        p = torch.softmax(s, dim=-1)
+        oc = torch.einsum("bhqk,bkhd->bqhd", p, v)
+        dD = (doc * oc).sum(-1).transpose(1, 2)  # [B, H, c]
+        # key rows of the sample: their columns of P and dS
+        pk = p[..., krows]
+        dsk = pk * (torch.einsum("bqhd,bkhd->bhqk", doc, vr) - dD[..., None])
+        dv += torch.einsum("bhqk,bqhd->bkhd", pk, doc)
+        dk += torch.einsum("bhqk,bqhd->bkhd", dsk, qc) * scale
+        # query rows of the sample inside this chunk
+        sel = qsel[c0 : c0 + chunk].nonzero()[:, 0]
+        if sel.numel():
+            ps = p[:, :, sel]
+            dss = ps * (torch.einsum("bqhd,bkhd->bhqk", doc[:, sel], v) - dD[:, :, sel, None])
+            dq[:, done : done + sel.numel()] = torch.einsum("bhqk,bkhd->bqhd", dss, k) * scale
+            done += sel.numel()
+    return dq, dk, dv
+
+
 # ------------------------------------------------------------ rope tables --
 
 

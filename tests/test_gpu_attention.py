@@ -300,3 +300,37 @@ def test_random_shapes_forward_backward(pkg, B, Sq, Sk, H):
         parity(qd.grad, dq, name=f"dq {tag}")
         parity(kvd.grad[:, :, 0], dk, name=f"dk {tag}")
         parity(kvd.grad[:, :, 1], dv, name=f"dv {tag}")
+
+
+@pytest.mark.parametrize("B,S,H", [(1, 16384, 2), (2, 12288, 1)])
+def test_long_sequence_sampled_rows(pkg, B, S, H):
+    """Long sequences (hundreds of key tiles; the split-key path for the last round): the
+    full kernel against the oracle on 96 sampled query rows of every (batch, head)."""
+    g = torch.Generator().manual_seed(S + H)
+    q, k, v = _qkv(B, S, S, H, seed=S + B)
+    out, lse = torch.ops.anima_flat.fa_fwd(*_gpu(q, k, v))
+    torch.cuda.synchronize()
+    rows = torch.randperm(S, generator=g)[:96].sort().values
+    eo, el = ref.attention_lse(q[:, rows], k, v)
+    parity(out[:, rows].reshape(B, 96, H, 128), eo, name=f"long S{S} B{B} H{H}")
+    parity(lse[:, :, rows], el, **LSE_TOL, name=f"long lse S{S}")
+
+
+def test_long_sequence_backward_sampled_rows(pkg):
+    """Backward at 16384 tokens (256 key tiles per dQ block, 128 query tiles per dK/dV block):
+    dQ on 64 sampled query rows and dK/dV on 64 sampled key rows against the chunked
+    closed-form oracle."""
+    B, S, H = 1, 16384, 1
+    q, k, v = _qkv(B, S, S, H, seed=16385)
+    g = torch.Generator().manual_seed(16386)
+    dout = ref.bf16_normal((B, S, H, 128), g)
+    qd, kd, vd = (t.requires_grad_(True) for t in _gpu(q, k, v))
+    out = pkg.attention(qd, kd, vd)
+    out.backward(dout.to("cuda", BF).reshape(out.shape))
+    torch.cuda.synchronize()
+    qrows = torch.randperm(S, generator=g)[:64].sort().values
+    krows = torch.cat([torch.randperm(S - 1, generator=g)[:63].sort().values, torch.tensor([S - 1])])
+    dq, dk, dv = ref.attention_backward_rows(q, k, v, dout, qrows, krows)
+    parity(qd.grad[:, qrows], dq, name="long dq")
+    parity(kd.grad[:, krows], dk, name="long dk")
+    parity(vd.grad[:, krows], dv, name="long dv")
