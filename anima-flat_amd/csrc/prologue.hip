@@ -188,9 +188,9 @@ constexpr int kBwdGroups = kBwdThreads / 8;  // 32 sections in flight per block
 
 // One block per chunk of `rows` consecutive tokens. Normalised sections per
 // token: NWHICH*H (q then k for the QKV prologue, one set for head_norm).
-// Group g handles sections g, g+32, ... of every token in the chunk and keeps
-// per-lane weight-gradient sums for each of the NWHICH weights; the block
-// then reduces them over groups in a fixed order into
+// Group g handles items g, g+32, ... of the chunk's (token, section) pairs
+// and keeps per-lane weight-gradient sums for each of the NWHICH weights; the
+// block then reduces them over groups in a fixed order into
 // partial[chunk][which][128].
 template <bool ROTATE, int NWHICH>
 __global__ __launch_bounds__(kBwdThreads) void norm_bwd_kernel(
@@ -212,25 +212,37 @@ __global__ __launch_bounds__(kBwdThreads) void norm_bwd_kernel(
     for (int i = 0; i < 16; ++i) acc[wi][i] = 0.f;
 
   const int64_t first = (int64_t)blockIdx.x * rows;
-  for (int r = 0; r < rows; ++r) {
+  const int nrows = (int)(ntok - first < rows ? ntok - first : rows);
+  // The chunk's (token, section) pairs in token-major order, dealt to the
+  // groups round-robin, so every group works whatever H is (head_norm has
+  // 16 sections per token for 32 groups).
+  const int per_tok = NWHICH * H;
+  int r = g / per_tok;
+  int sec = g - r * per_tok;
+  while (r < nrows) {
     const int64_t token = first + r;
-    if (token >= ntok) break;
+    const int which = sec / H;
+    const int head = sec - which * H;
+    const bf16* src = x + token * xrow + which * width + head * kHd;
+    const bf16* dy = (which == 0 ? dy0 : dy1) + token * width + head * kHd;
+    bf16* out = dx + token * xrow + which * width + head * kHd;
+    const float* w = which == 0 ? w0 : w1;
     const int64_t pos = token % S;
-    for (int sec = g; sec < NWHICH * H; sec += kBwdGroups) {
-      const int which = sec / H;
-      const int head = sec - which * H;
-      const bf16* src = x + token * xrow + which * width + head * kHd;
-      const bf16* dy = (which == 0 ? dy0 : dy1) + token * width + head * kHd;
-      bf16* out = dx + token * xrow + which * width + head * kHd;
-      const float* w = which == 0 ? w0 : w1;
-      if (NWHICH == 1 || which == 0) {
-        norm_section_bwd<ROTATE>(src, dy, out, w, cos, sin, pos, j, eps, acc[0], acc[0] + 8);
-      } else {
-        norm_section_bwd<ROTATE>(src, dy, out, w, cos, sin, pos, j, eps, acc[NWHICH - 1],
-                                 acc[NWHICH - 1] + 8);
-      }
+    if (NWHICH == 1 || which == 0) {
+      norm_section_bwd<ROTATE>(src, dy, out, w, cos, sin, pos, j, eps, acc[0], acc[0] + 8);
+    } else {
+      norm_section_bwd<ROTATE>(src, dy, out, w, cos, sin, pos, j, eps, acc[NWHICH - 1],
+                               acc[NWHICH - 1] + 8);
     }
-    if (dv) {  // dV passes through the prologue unchanged: copy it into dqkv.
+    sec += kBwdGroups;
+    while (sec >= per_tok) {
+      sec -= per_tok;
+      ++r;
+    }
+  }
+  if (dv) {  // dV passes through the prologue unchanged: copy it into dqkv.
+    for (int rr = 0; rr < nrows; ++rr) {
+      const int64_t token = first + rr;
       for (int c = tid; c < (int)(width / 8); c += kBwdThreads) {
         st16(dx + token * xrow + 2 * width + 8 * c, ld16(dv + token * width + 8 * c));
       }
