@@ -19,7 +19,7 @@ from .attention import attention, cross_attention_trimmed, use_fa4  # noqa: F401
 from .context import Context, context_lengths, rope_tables, trim_context  # noqa: F401
 from .kernels.ctx_scale import ctx_scale  # noqa: F401
 from .kernels.fp8 import rowquant  # noqa: F401
-from .kernels.rope import head_norm, qkv_norm_rope  # noqa: F401
+from .kernels.rope import head_norm, qkv_norm_rope, qkv_proj_norm_rope  # noqa: F401
 
 __all__ = [
     "Context",
@@ -29,6 +29,7 @@ __all__ = [
     "ctx_scale",
     "head_norm",
     "qkv_norm_rope",
+    "qkv_proj_norm_rope",
     "rope_tables",
     "rowquant",
     "trim_context",

@@ -35,6 +35,11 @@ _PROTOTYPES: dict[str, tuple[object, list[object]]] = {
         c_int,
         [c_void_p] * 4 + [c_void_p] * 4 + [_I64] * 4 + [c_float, c_int, c_void_p],
     ),
+    "aa_qkv_proj_norm_rope": (
+        c_int,
+        [c_void_p, _I64, c_void_p] + [c_void_p] * 3 + [c_void_p] * 4 + [_I64] * 4
+        + [c_float, c_int, c_void_p],
+    ),
     "aa_head_norm_fwd": (c_int, [c_void_p] * 3 + [_I64] * 4 + [c_float, c_int, c_void_p]),
     "aa_qkv_norm_rope_bwd_workspace": (c_size_t, [_I64] * 4),
     "aa_qkv_norm_rope_bwd": (

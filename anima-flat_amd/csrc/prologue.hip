@@ -10,80 +10,20 @@
 // These kernels are HBM-bound: per section they read 256 B and write 256 B;
 // cos/sin rows (2 x 256 B per token) and the weights stay in L2/L1.
 #include "aa_common.h"
+#include "norm_rope.h"
 
 namespace aa {
 
-constexpr int kHd = 128;
-constexpr int kHalf = 64;
-
-struct Section {
-  float a[8];
-  float b[8];
-};
-
-__device__ __forceinline__ void load_section(const bf16* src, int j, Section& s) {
-  unpack8(ld16(src + 8 * j), s.a);
-  unpack8(ld16(src + kHalf + 8 * j), s.b);
-}
-
-__device__ __forceinline__ void load_w(const float* w, int j, float* wa, float* wb) {
-  f32x4 w0 = ldf4(w + 8 * j), w1 = ldf4(w + 8 * j + 4);
-  f32x4 w2 = ldf4(w + kHalf + 8 * j), w3 = ldf4(w + kHalf + 8 * j + 4);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    wa[i] = w0[i];
-    wa[i + 4] = w1[i];
-    wb[i] = w2[i];
-    wb[i + 4] = w3[i];
-  }
-}
-
-__device__ __forceinline__ void load_rot(const float* cos, const float* sin, int64_t pos, int j,
-                                         float* c, float* s) {
-  const float* cp = cos + pos * kHalf + 8 * j;
-  const float* sp = sin + pos * kHalf + 8 * j;
-  f32x4 c0 = ldf4(cp), c1 = ldf4(cp + 4), s0 = ldf4(sp), s1 = ldf4(sp + 4);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    c[i] = c0[i];
-    c[i + 4] = c1[i];
-    s[i] = s0[i];
-    s[i + 4] = s1[i];
-  }
-}
-
 // Forward of one section: rstd over 128 values, y = bf16(x * rstd * w), then
-// optional rotation out_a = y_a cos - y_b sin, out_b = y_b cos + y_a sin
-// (the order of src/kernels/rope.py:39-58).
+// optional rotation (norm_rotate), bf16 store.
 template <bool ROTATE>
 __device__ __forceinline__ void norm_section(const bf16* src, bf16* dst, const float* w,
                                              const float* cos, const float* sin, int64_t pos,
                                              int j, float eps) {
   Section x;
   load_section(src, j, x);
-  float ss = 0.f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) ss += x.a[i] * x.a[i] + x.b[i] * x.b[i];
-  ss = group_sum<8>(ss);
-  const float rstd = rsqrtf(ss / (float)kHd + eps);
-  float wa[8], wb[8];
-  load_w(w, j, wa, wb);
   float oa[8], ob[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    oa[i] = round_bf16(x.a[i] * rstd * wa[i]);
-    ob[i] = round_bf16(x.b[i] * rstd * wb[i]);
-  }
-  if constexpr (ROTATE) {
-    float c[8], s[8];
-    load_rot(cos, sin, pos, j, c, s);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float ya = oa[i], yb = ob[i];
-      oa[i] = ya * c[i] - yb * s[i];
-      ob[i] = yb * c[i] + ya * s[i];
-    }
-  }
+  norm_rotate<ROTATE>(x, w, cos, sin, pos, j, eps, oa, ob);
   st16(dst + 8 * j, pack8(oa));
   st16(dst + kHalf + 8 * j, pack8(ob));
 }

@@ -82,6 +82,24 @@ int aa_qkv_norm_rope_fwd(const void* qkv, void* q, void* k, void* v,
                          float eps, int dtype, void* stream);
 
 /*
+ * QKV projection fused with the prologue: q, k, v = aa_qkv_norm_rope_fwd of
+ * qkv = hid @ weight^T (bf16), without qkv ever reaching memory.
+ *   hid [B*S rows, H*hd], row r at hid + r * hid_row_stride elements
+ *   (hid_row_stride >= H*hd, a multiple of 8); weight [3*H*hd, H*hd]
+ *   contiguous (nn.Linear layout, no bias); q, k, v [B, S, H, hd] contiguous
+ *   outputs (v is the projection's V section as it is); q_weight, k_weight,
+ *   cos, sin as for aa_qkv_norm_rope_fwd. H <= 64.
+ * Replaces: src/model.py:308-316 (b.qkv(hid), model.py:134, followed by
+ *           qkv_norm_rope, src/kernels/rope.py:616-645) on the inference path.
+ */
+int aa_qkv_proj_norm_rope(const void* hid, int64_t hid_row_stride, const void* weight,
+                          void* q, void* k, void* v,
+                          const float* q_weight, const float* k_weight,
+                          const float* cos, const float* sin,
+                          int64_t B, int64_t S, int64_t H, int64_t hd,
+                          float eps, int dtype, void* stream);
+
+/*
  * Per-head RMSNorm: x [B, S, H*hd] contiguous -> y [B, S, H, hd] contiguous.
  * Replaces: src/kernels/rope.py:203-212 (_head_norm), kernel rope.py:146-172.
  */

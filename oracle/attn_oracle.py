@@ -88,6 +88,25 @@ def qkv_norm_rope(
     return q, k, x[:, :, 2]
 
 
+def qkv_proj_norm_rope(
+    hid: torch.Tensor,
+    weight: torch.Tensor,
+    q_weight: torch.Tensor,
+    k_weight: torch.Tensor,
+    cos: torch.Tensor,
+    sin: torch.Tensor,
+    heads: int,
+    eps: float = 1e-5,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """(q, k, v) of the block's QKV projection followed by the prologue
+    (src/model.py:308-316): qkv = hid @ weight^T (nn.Linear without bias,
+    model.py:134) accumulated in float32 and rounded to bf16, as the bf16 GEMM
+    writes it, then `qkv_norm_rope`; v is the bf16 projection output."""
+    qkv = (hid.float() @ weight.float().T).to(BF16)
+    q, k, v = qkv_norm_rope(qkv, q_weight, k_weight, cos, sin, heads, eps)
+    return q, k, v.to(BF16)
+
+
 def head_norm(
     x: torch.Tensor,
     weight: torch.Tensor,

@@ -205,6 +205,30 @@ def test_rotation_norms_identity_and_relative_position():
         torch.testing.assert_close(diag, diag[:1].expand_as(diag))
 
 
+def test_qkv_projection_orientation_closed_form():
+    """The fused-projection oracle with W = [P; I; 2I] (P a permutation, not
+    symmetric): the q section is hid permuted by P's rows (a transposed weight
+    would apply the inverse permutation), k is hid itself, v is exactly 2 hid."""
+    g = torch.Generator().manual_seed(5)
+    B, S, H = 2, 6, 2
+    D = H * 128
+    hid = ref.bf16_normal((B, S, D), g)
+    perm = torch.randperm(D, generator=g)
+    assert not torch.equal(perm, torch.argsort(perm))
+    P = torch.zeros(D, D)
+    P[torch.arange(D), perm] = 1.0
+    w = torch.cat([P, torch.eye(D), 2 * torch.eye(D)]).to(torch.bfloat16)
+    qw, kw = ref.norm_weight(128, g), ref.norm_weight(128, g)
+    cos, sin = ref.rope_tables(2, 3, 128)
+    q, k, v = ref.qkv_proj_norm_rope(hid, w, qw, kw, cos, sin, H, 1e-6)
+    qkv = torch.cat([hid[..., perm], hid, 2 * hid], dim=-1)
+    eq, ek, _ = ref.qkv_norm_rope(qkv, qw, kw, cos, sin, H, 1e-6)
+    assert torch.equal(q, eq) and torch.equal(k, ek)
+    assert torch.equal(v.float(), (2 * hid.float()).reshape(B, S, H, 128))
+    wrong = torch.cat([hid[..., torch.argsort(perm)], hid, 2 * hid], dim=-1)
+    assert not torch.equal(q, ref.qkv_norm_rope(wrong, qw, kw, cos, sin, H, 1e-6)[0])
+
+
 def test_rope_table_structure():
     cos, sin = ref.rope_tables(4, 6, 128)
     assert cos.shape == (24, 64)
