@@ -354,6 +354,25 @@ def main() -> int:
             extras["prologue_cfg5_bwd"] = {"us": round(us_pb * 1e3, 2),
                                            "GB/s": round((9 * sec + 2 * S * 64 * 4) / (us_pb * 1e-3) / 1e9, 1)}
 
+            # The block's QKV projection + prologue at config 2 (random-init bf16
+            # weight [6144, 2048]): fused kernel vs torch's GEMM (hipBLASLt) +
+            # qkv_norm_rope.
+            hid = torch.randn(B, S, H * d, device=dev, dtype=BF)
+            wq = (torch.randn(3 * H * d, H * d, device=dev) * (H * d) ** -0.5).to(BF)
+            proj_fused = lambda: pkg.qkv_proj_norm_rope(hid, wq, p["q_weight"], p["k_weight"], p["cos"], p["sin"], H, eps)
+            proj_split = lambda: pkg.qkv_norm_rope(torch.nn.functional.linear(hid, wq), p["q_weight"],
+                                                   p["k_weight"], p["cos"], p["sin"], H, eps)
+            prewarm(proj_fused, 0.2)
+            us_fu, us_sp = time_graph(proj_fused), time_graph(proj_split)
+            gemm_flops = 2 * B * S * (H * d) * 3 * (H * d)
+            extras["qkv_proj_cfg2"] = {
+                "fused_us": round(us_fu * 1e3, 2),
+                "fused_TFLOP/s": round(gemm_flops / (us_fu * 1e-3) / 1e12, 1),
+                "linear_plus_prologue_us": round(us_sp * 1e3, 2),
+                "what": "qkv_proj_norm_rope vs F.linear (hipBLASLt) + qkv_norm_rope, B=1, 4096 tokens",
+            }
+            del hid, wq
+
         # Config 5: forward + backward (LoRA training attention), B=1, 4096.
         qg, kg, vg = (t.detach().clone().requires_grad_(True) for t in (q, k, v.contiguous()))
         dout = torch.randn(B, S, H * d, device=dev, dtype=BF)
