@@ -6,38 +6,41 @@
 // a 3 * H * 128 * 2-byte round trip per token through HBM between the two.
 // Here the projection's output tile never leaves the chip:
 //
-//   out tile = 256 tokens x 128 columns = one (q | k | v, head) section of 256
-//   tokens; acc = X[256 x K] . W[128 x K]^T in fp32 on v_mfma_f32_32x32x16_bf16,
-//   rounded to bf16 (the value the reference's GEMM writes), staged in LDS,
-//   then per token RMSNorm + rotation (norm_rotate, the prologue's math) for
-//   q and k, a copy for v, and 256-byte row stores into q, k, v [ntok, H, 128].
+//   out tile = 256 tokens x 256 columns = two (q | k | v, head) sections of
+//   256 tokens; acc = X[256 x K] . W[256 x K]^T in fp32 on
+//   v_mfma_f32_32x32x16_bf16, rounded to bf16 (the value the reference's GEMM
+//   writes), staged in LDS, then per token RMSNorm + rotation (norm_rotate,
+//   the prologue's math) for q and k, a copy for v, and 256-byte row stores
+//   into q, k, v [ntok, H, 128].
 //
-// Main loop: 8 waves, each a 64-token x 64-column block (2 x 2 accumulators),
-// over K in stages of 64: the stage's X rows (256 x 128 B) and W rows
-// (128 x 128 B) move HBM -> LDS by DMA (global_load_lds_dwordx4, no
-// registers) into a 3-stage ring, two stages ahead, one barrier per stage.
-// Tiles in LDS use the row-tile format of the attention kernels with 64-wide
-// rows: element (r, k) at (r >> 4) * 1024 + (k >> 3) * 128 + (r & 15) * 8
-// + (k & 7), so an operand read (16 lanes on one 16-byte chunk of 16
-// consecutive rows) covers 256 contiguous bytes.
+// Main loop: 8 waves, each 64 tokens x one 128-column section (2 x 4
+// accumulators: 6 operand reads per 8 MFMAs), over K in stages of 32: the
+// stage's X and W rows (2 x 256 x 64 B) move HBM -> LDS by DMA
+// (global_load_lds_dwordx4, no registers) into a 4-stage ring, three stages
+// ahead, one barrier per stage. Tiles in LDS use the row-tile format of the
+// attention kernels with 32-wide rows: element (r, k) at (r >> 4) * 512
+// + (k >> 3) * 128 + (r & 15) * 8 + (k & 7), so an operand read (16 lanes on
+// one 16-byte chunk of 16 consecutive rows) covers 256 contiguous bytes and
+// one DMA instruction fills one 16-row group.
 //
 // Work order: workgroups go to XCDs in contiguous ranges (xcd_remap), and
 // within the range in groups of 4 token tiles x all column tiles, so the 32
 // workgroups an XCD runs at once share 4 X tiles and 8 W tiles in its L2.
+// With an odd number of sections (3 H) the last column tile holds one.
 #include "aa_common.h"
 #include "norm_rope.h"
 #include "tile_io.h"
 
 namespace aa {
 
-constexpr int kPM = 256;                        // tokens per workgroup
-constexpr int kPN = 128;                        // output columns per workgroup (one section)
-constexpr int kPK = 64;                         // K per stage
-constexpr int kPStages = 3;
+constexpr int kPM = 256;                            // tokens per workgroup
+constexpr int kPN = 256;                            // output columns: two sections
+constexpr int kPK = 32;                             // K per stage
+constexpr int kPStages = 4;
 constexpr int kPThreads = 512;
-constexpr int kPXElems = kPM * kPK;             // 32 KiB
+constexpr int kPXElems = kPM * kPK;                 // 16 KiB
 constexpr int kPStageElems = kPXElems + kPN * kPK;  // + 16 KiB of W
-constexpr int kPGroupM = 4;                     // token tiles per work-order group
+constexpr int kPGroupM = 4;                         // token tiles per work-order group
 
 struct ProjParams {
   const bf16* x;  // hidden states, row r at x + r * xs
@@ -58,17 +61,14 @@ struct ProjParams {
   float eps;
 };
 
-// DMA of row group g (16 rows x 64 k) of a tile whose row 0 is at `base`
-// (row stride rs elements, already offset to the stage's k): two 1 KiB
-// blocks, chunks 0-3 and 4-7 of the same rows. Rows at or past `nrows` re-read
-// row nrows - 1 (their results are not stored).
+// DMA of row group g (16 rows x 32 k, 1 KiB) of a tile whose row 0 is at
+// `base` (row stride rs elements, already offset to the stage's k): lane
+// moves chunk lane >> 4 of row 16 g + (lane & 15). Rows at or past `nrows`
+// re-read row nrows - 1 (their results are not stored).
 __device__ __forceinline__ void dma_proj_group(const bf16* base, int64_t rs, int nrows,
                                                bf16* tile, int g, int lane) {
   const int row = min(16 * g + (lane & 15), nrows - 1);
-  const bf16* src = base + (int64_t)row * rs + 8 * (lane >> 4);
-  bf16* dst = tile + g * 1024;
-  dma16_off<0>(src, dst);
-  dma16_off<64>(src, dst + 512);
+  dma16_off<0>(base + (int64_t)row * rs + 8 * (lane >> 4), tile + g * 512);
 }
 
 __global__ __launch_bounds__(kPThreads) void qkv_proj_kernel(ProjParams p) {
@@ -77,8 +77,9 @@ __global__ __launch_bounds__(kPThreads) void qkv_proj_kernel(ProjParams p) {
   const int lane = tid & 63;
   const int wave = tid >> 6;
 
-  // Tile of this workgroup.
-  const int ntn = 3 * p.H;
+  // Tile of this workgroup: token tile mt, sections 2 nt and 2 nt + 1.
+  const int nsec = 3 * p.H;
+  const int ntn = (nsec + 1) / 2;
   const int total = p.mtiles * ntn;
   const int L = xcd_remap(blockIdx.x, total);
   const int group = L / (kPGroupM * ntn);
@@ -89,109 +90,122 @@ __global__ __launch_bounds__(kPThreads) void qkv_proj_kernel(ProjParams p) {
 
   const int64_t row0 = (int64_t)mt * kPM;
   const int nrows = (int)min<int64_t>(kPM, p.ntok - row0);
+  const int ncols = min(kPN, (nsec - 2 * nt) * kHd);
   const bf16* xbase = p.x + row0 * p.xs;
   const bf16* wbase = p.w + (int64_t)nt * kPN * p.K;
 
-  // Stage s -> ring slot s % 3; wave w moves X row groups 2w, 2w + 1 and W row group w.
+  // Stage s -> ring slot s % 4; wave w moves X and W row groups 2w, 2w + 1.
   auto issue = [&](int s) {
     bf16* st = lds + (s % kPStages) * kPStageElems;
     const int k0 = s * kPK;
     dma_proj_group(xbase + k0, p.xs, nrows, st, 2 * wave, lane);
     dma_proj_group(xbase + k0, p.xs, nrows, st, 2 * wave + 1, lane);
-    dma_proj_group(wbase + k0, p.K, kPN, st + kPXElems, wave, lane);
+    dma_proj_group(wbase + k0, p.K, ncols, st + kPXElems, 2 * wave, lane);
+    dma_proj_group(wbase + k0, p.K, ncols, st + kPXElems, 2 * wave + 1, lane);
   };
 
   const int nk = p.K / kPK;
   issue(0);
   if (nk > 1) issue(1);
+  if (nk > 2) issue(2);
 
   const int wm = wave & 3;   // tokens 64 wm .. 64 wm + 63
-  const int wn = wave >> 2;  // columns 64 wn .. 64 wn + 63
+  const int wn = wave >> 2;  // section 2 nt + wn: columns 128 wn .. 128 wn + 127
   const int li = lane & 31;
   const int hh = lane >> 5;
-  // Row 32 t + li of a 64-row block, chunk 2 kk + hh: rd + 2048 t + 256 kk.
-  const int rd = (li >> 4) * 1024 + (li & 15) * 8 + hh * 128;
+  // Row 32 t + li of a row block, chunk 2 kk + hh: rd + 1024 t + 256 kk.
+  const int rd = (li >> 4) * 512 + (li & 15) * 8 + hh * 128;
 
-  f32x16 acc[2][2];
+  f32x16 acc[4][2];
 #pragma unroll
-  for (int c = 0; c < 2; ++c)
+  for (int c = 0; c < 4; ++c)
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[c][t][e] = 0.f;
 
   for (int s = 0; s < nk; ++s) {
-    // This wave's DMAs of stage s are done once at most the 6 of stage s + 1
-    // are outstanding; the barrier then publishes every wave's and retires
-    // all reads of stage s - 1, whose slot the DMA of stage s + 2 reuses.
-    if (s + 1 < nk) {
-      asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+    // This wave's DMAs of stage s are done once at most those of the stages
+    // after it (4 each) are outstanding; the barrier then publishes every
+    // wave's and retires all reads of stage s - 1, whose slot the DMA of
+    // stage s + 3 reuses.
+    if (s + 2 < nk) {
+      asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    } else if (s + 1 < nk) {
+      asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
     } else {
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
     __syncthreads();
-    if (s + 2 < nk) issue(s + 2);
-    const bf16* xs = lds + (s % kPStages) * kPStageElems + wm * 4096 + rd;
+    if (s + 3 < nk) issue(s + 3);
+    const bf16* xs = lds + (s % kPStages) * kPStageElems + wm * 2048 + rd;
     const bf16* ws = lds + (s % kPStages) * kPStageElems + kPXElems + wn * 4096 + rd;
 #pragma unroll
     for (int kk = 0; kk < kPK / 16; ++kk) {
-      const bf16x8 a0 = *reinterpret_cast<const bf16x8*>(ws + 256 * kk);
-      const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(ws + 2048 + 256 * kk);
-      const bf16x8 b0 = *reinterpret_cast<const bf16x8*>(xs + 256 * kk);
-      const bf16x8 b1 = *reinterpret_cast<const bf16x8*>(xs + 2048 + 256 * kk);
-      acc[0][0] = mfma32(a0, b0, acc[0][0]);
-      acc[0][1] = mfma32(a0, b1, acc[0][1]);
-      acc[1][0] = mfma32(a1, b0, acc[1][0]);
-      acc[1][1] = mfma32(a1, b1, acc[1][1]);
+      bf16x8 a[4], b[2];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) a[c] = *reinterpret_cast<const bf16x8*>(ws + 1024 * c + 256 * kk);
+#pragma unroll
+      for (int t = 0; t < 2; ++t) b[t] = *reinterpret_cast<const bf16x8*>(xs + 1024 * t + 256 * kk);
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int t = 0; t < 2; ++t) acc[c][t] = mfma32(a[c], b[t], acc[c][t]);
     }
   }
-  __syncthreads();  // every wave is done with the ring: reuse it as the output tile
+  __syncthreads();  // every wave is done with the ring: reuse it as the output tiles
 
   // acc[c][t] holds out^T: lane li is token 64 wm + 32 t + li, element e is
-  // column 64 wn + 32 c + 8 (e / 4) + 4 hh + (e % 4). Staged as bf16 rows of
-  // 128 columns, 16-byte chunk ch of row r at r * 128 + ((ch ^ (r & 15)) * 8).
-  bf16* tile = lds;
+  // column 32 c + 8 (e / 4) + 4 hh + (e % 4) of section wn. Staged as bf16
+  // rows of 128 columns per section, 16-byte chunk ch of row r at
+  // r * 128 + ((ch ^ (r & 15)) * 8).
+  bf16* mine = lds + wn * (kPM * kHd);
 #pragma unroll
-  for (int c = 0; c < 2; ++c)
+  for (int c = 0; c < 4; ++c)
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       const int r = 64 * wm + 32 * t + li;
 #pragma unroll
       for (int e4 = 0; e4 < 4; ++e4) {
-        const int ch = 8 * wn + 4 * c + e4;
+        const int ch = 4 * c + e4;
         u32x2 w2;
         w2[0] = pack_bf16(acc[c][t][4 * e4], acc[c][t][4 * e4 + 1]);
         w2[1] = pack_bf16(acc[c][t][4 * e4 + 2], acc[c][t][4 * e4 + 3]);
-        *reinterpret_cast<u32x2*>(tile + r * 128 + ((ch ^ (r & 15)) * 8) + 4 * hh) = w2;
+        *reinterpret_cast<u32x2*>(mine + r * 128 + ((ch ^ (r & 15)) * 8) + 4 * hh) = w2;
       }
     }
   __syncthreads();
 
-  // Per token: the section's RMSNorm + rotation (q, k) or a copy (v), 8 lanes
-  // per token, two 16-byte chunks per lane, 256-byte rows out.
+  // Per (token, section): RMSNorm + rotation (q, k) or a copy (v), 8 lanes
+  // per item, two 16-byte chunks per lane, 256-byte rows out.
   const int j = tid & 7;
   const int grp = tid >> 3;
-  const int seg = nt / p.H;
-  const int head = nt - seg * p.H;
-  bf16* out = seg == 0 ? p.q : (seg == 1 ? p.k : p.v);
-  const float* nw = seg == 0 ? p.qw : p.kw;
-  for (int r = grp; r < nrows; r += kPThreads / 8) {
-    const u32x4 ra = *reinterpret_cast<const u32x4*>(tile + r * 128 + ((j ^ (r & 15)) * 8));
-    const u32x4 rb =
-        *reinterpret_cast<const u32x4*>(tile + r * 128 + (((8 + j) ^ (r & 15)) * 8));
-    const int64_t token = row0 + r;
-    bf16* dst = out + (token * p.H + head) * kHd;
-    if (seg == 2) {
-      st16(dst + 8 * j, ra);
-      st16(dst + kHalf + 8 * j, rb);
-    } else {
-      Section x;
-      unpack8(ra, x.a);
-      unpack8(rb, x.b);
-      float oa[8], ob[8];
-      norm_rotate<true>(x, nw, p.cos, p.sin, token % p.S, j, p.eps, oa, ob);
-      st16(dst + 8 * j, pack8(oa));
-      st16(dst + kHalf + 8 * j, pack8(ob));
+  const int nmine = ncols / kHd;
+  for (int sc = 0; sc < nmine; ++sc) {
+    const int gsec = 2 * nt + sc;
+    const int seg = gsec / p.H;
+    const int head = gsec - seg * p.H;
+    bf16* out = seg == 0 ? p.q : (seg == 1 ? p.k : p.v);
+    const float* nw = seg == 0 ? p.qw : p.kw;
+    const bf16* tile = lds + sc * (kPM * kHd);
+    for (int r = grp; r < nrows; r += kPThreads / 8) {
+      const u32x4 ra = *reinterpret_cast<const u32x4*>(tile + r * 128 + ((j ^ (r & 15)) * 8));
+      const u32x4 rb =
+          *reinterpret_cast<const u32x4*>(tile + r * 128 + (((8 + j) ^ (r & 15)) * 8));
+      const int64_t token = row0 + r;
+      bf16* dst = out + (token * p.H + head) * kHd;
+      if (seg == 2) {
+        st16(dst + 8 * j, ra);
+        st16(dst + kHalf + 8 * j, rb);
+      } else {
+        Section x;
+        unpack8(ra, x.a);
+        unpack8(rb, x.b);
+        float oa[8], ob[8];
+        norm_rotate<true>(x, nw, p.cos, p.sin, token % p.S, j, p.eps, oa, ob);
+        st16(dst + 8 * j, pack8(oa));
+        st16(dst + kHalf + 8 * j, pack8(ob));
+      }
     }
   }
 }
@@ -220,7 +234,7 @@ extern "C" int aa_qkv_proj_norm_rope(const void* hid, int64_t hid_row_stride, co
     return fail(AA_EINVAL, "qkv_proj: pointers must be 16-byte aligned");
   const int64_t ntok = B * S;
   const int64_t mtiles = (ntok + kPM - 1) / kPM;
-  const int64_t total = mtiles * 3 * H;
+  const int64_t total = mtiles * ((3 * H + 1) / 2);
   if (total > 0x7fffffff) return fail(AA_EUNSUPPORTED, "qkv_proj: too many tokens");
   ProjParams p;
   p.x = (const bf16*)hid;
