@@ -115,6 +115,13 @@ def test_invalid_arguments_fail_before_any_launch(pkg, lib):
     assert lib.aa_attn_bwd(ctypes.byref(b), None, 0, None) == L.AA_EINVAL
     assert lib.aa_qkv_norm_rope_fwd(None, None, None, None, None, None, None, None, 1, 4, 2, 128, 1e-6, 0, None) == L.AA_EINVAL
     assert lib.aa_head_norm_fwd(None, None, None, 1, 4, 2, 96, 1e-6, 0, None) == L.AA_EUNSUPPORTED
+    proj = lambda H, hd, dtype, B=1, rs=256: lib.aa_qkv_proj_norm_rope(
+        None, rs, None, None, None, None, None, None, None, None, B, 4, H, hd, 1e-6, dtype, None)
+    assert proj(2, 96, 0) == L.AA_EUNSUPPORTED  # head_dim
+    assert proj(2, 128, 1) == L.AA_EUNSUPPORTED  # dtype
+    assert proj(65, 128, 0) == L.AA_EINVAL  # H > 64
+    assert proj(2, 128, 0) == L.AA_EINVAL  # null pointers
+    assert proj(2, 128, 0, B=0) == L.AA_OK  # no tokens: nothing to do
     assert lib.aa_ctx_scale_fwd(None, None, None, None, 1, 4, 2, 128, 3, None) == L.AA_EUNSUPPORTED
     assert lib.aa_context_lengths(None, 1, 8, 8, 64, 8, 3, None, None, None, 0, None) == L.AA_EUNSUPPORTED
     assert lib.aa_context_lengths(None, 1, 8, 8, 64, 8, 2, None, None, None, 0, None) == L.AA_EINVAL
@@ -146,13 +153,17 @@ def test_cpu_tensors_are_rejected(pkg):
         pkg.context_lengths(torch.zeros(1, 4, 8, dtype=torch.bfloat16))
     with pytest.raises(ValueError, match="CUDA tensors required"):
         pkg.rowquant(torch.zeros(1, 4, 8, dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="CUDA"):
+        pkg.qkv_proj_norm_rope(torch.zeros(1, 4, 256, dtype=torch.bfloat16),
+                               torch.zeros(768, 256, dtype=torch.bfloat16), torch.ones(128),
+                               torch.ones(128), torch.zeros(4, 64), torch.zeros(4, 64), 2)
     assert pkg.use_fa4(q) is False
 
 
 def test_ops_are_registered_with_reference_names(pkg):
     for name in ("fa_fwd", "fa_fwd_nolse", "fa_fwd_k", "fa_bwd", "qkv_norm_rope", "qkv_norm_rope_v",
                  "qkv_norm_rope_bwd", "head_norm", "head_norm_bwd", "ctx_scale", "ctx_scale_bwd",
-                 "rowquant"):
+                 "rowquant", "qkv_proj_norm_rope"):
         assert hasattr(torch.ops.anima_flat, name), name
 
 
@@ -182,6 +193,10 @@ def test_fake_shapes_on_meta_tensors(pkg):
     x = torch.empty(B, Sq, 2048, dtype=torch.bfloat16, device="meta")
     qx, sx = torch.ops.anima_flat.rowquant(x, False)
     assert qx.shape == x.shape and qx.dtype == torch.float8_e4m3fn and sx.shape == (B * Sq, 1)
+    hid = torch.empty(B, Sq, H * 128, dtype=torch.bfloat16, device="meta")
+    wq = torch.empty(3 * H * 128, H * 128, dtype=torch.bfloat16, device="meta")
+    outs = torch.ops.anima_flat.qkv_proj_norm_rope(hid, wq, w, w, cos, cos, H, 1e-6)
+    assert all(t.shape == (B, Sq, H, 128) and t.dtype == torch.bfloat16 for t in outs)
 
 
 def test_rope_tables_bit_identical_to_oracle(pkg):
