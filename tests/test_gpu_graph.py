@@ -33,6 +33,8 @@ def test_graph_replays_match_eager(pkg):
     ctx = torch.zeros(B, 96, 64, dtype=BF, device=dev)
     ctx[0, :40] = 1.0
     ctx[1, :71] = -2.0
+    hid = ref.bf16_normal((B, S, H * d), g).to(dev, BF)
+    wqkv = (torch.randn(3 * H * d, H * d, generator=g) * (H * d) ** -0.5).to(dev, BF)
 
     def step():
         q, k, v = pkg.qkv_norm_rope(qkv, qw, kw, cos, sin, H, 1e-6)
@@ -41,7 +43,8 @@ def test_graph_replays_match_eager(pkg):
         seq, lnp = pkg.context_lengths(ctx)
         o_cross = pkg.cross_attention_trimmed(qx, kc, vc, seq, lnp)
         oq, os_ = pkg.rowquant(o_self)
-        return [o_self, o_cross, oq.view(torch.uint8), os_, seq, lnp]
+        pq, pk, pv = pkg.qkv_proj_norm_rope(hid, wqkv, qw, kw, cos, sin, H, 1e-6)
+        return [o_self, o_cross, oq.view(torch.uint8), os_, seq, lnp, pq, pk, pv]
 
     with torch.no_grad():
         eager = [t.clone() for t in step()]

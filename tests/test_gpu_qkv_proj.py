@@ -105,3 +105,11 @@ def test_qkv_proj_rejects_bad_inputs(pkg):
         pkg.qkv_proj_norm_rope(hid[:, :, :128], w, qw, qw, cs, cs, 2)
     with pytest.raises(RuntimeError, match="backward"):
         pkg.qkv_proj_norm_rope(hid.clone().requires_grad_(True), w, qw, qw, cs, cs, 2)
+
+
+def test_qkv_proj_deterministic(pkg):
+    hid, w, qw, kw, cos, sin = _inputs(1, 700, 16, seed=31)
+    a = _run(pkg, hid, w, qw, kw, cos, sin, 16, 1e-6)
+    b = _run(pkg, hid, w, qw, kw, cos, sin, 16, 1e-6)
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
