@@ -265,7 +265,7 @@ __global__ void zero_f32_kernel(float* __restrict__ a, float* __restrict__ b, in
   }
 }
 
-constexpr int kBwdRows = 4;  // tokens per block: enough blocks to keep the CUs' loads in flight
+constexpr int kBwdRows = 8;  // tokens per block: enough blocks to keep the CUs' loads in flight
 
 static int64_t bwd_chunks(int64_t B, int64_t S) { return (B * S + kBwdRows - 1) / kBwdRows; }
 static int64_t l1_blocks(int64_t nchunk) { return (nchunk + kL1Chunks - 1) / kL1Chunks; }
