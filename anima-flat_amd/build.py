@@ -44,6 +44,9 @@ DEVICE_FLAGS = [
 
 RESOURCE_REMARK = "-Rpass-analysis=kernel-resource-usage"
 
+# Per-source extra flags (none at present).
+SOURCE_FLAGS: dict[str, list[str]] = {}
+
 
 def hipcc() -> str:
     """Path of hipcc (ROCM_PATH/bin, then PATH)."""
@@ -57,13 +60,19 @@ def hipcc() -> str:
     return found
 
 
+SGPR_SPILL_WARNINGS: list[str] = []
+
+
 def _check_resources(stderr: str, src: str) -> None:
-    """Fails the build if any kernel of `src` uses scratch memory or spills VGPRs.
+    """Fails the build if any kernel of `src` uses scratch memory or spills VGPRs,
+    and records (and prints) every kernel that spills SGPRs.
 
     The remarks come from -Rpass-analysis=kernel-resource-usage. Every kernel
-    here is written to keep its working set in registers and LDS; a spill
+    here is written to keep its working set in registers and LDS; a VGPR spill
     means an unroll or an indexing pattern went wrong, and costs an order of
-    magnitude in speed, so it is treated as a build error."""
+    magnitude in speed, so it is treated as a build error. SGPR spills go to
+    VGPR lanes (v_writelane / v_readlane, no memory); they cost a few
+    instructions where they occur, so they are reported, not rejected."""
     name = None
     for line in stderr.splitlines():
         if "remark:" not in line:
@@ -75,6 +84,12 @@ def _check_resources(stderr: str, src: str) -> None:
             value = int(body.split(":", 1)[1].split("[")[0])
             if value != 0:
                 raise RuntimeError(f"{src}: kernel {name}: {body.split('[-R')[0].strip()}")
+        elif body.startswith("SGPRs Spill:"):
+            value = int(body.split(":", 1)[1].split("[")[0])
+            if value != 0:
+                msg = f"{src}: kernel {name}: {value} SGPRs spilled to VGPR lanes"
+                SGPR_SPILL_WARNINGS.append(msg)
+                print(f"warning: {msg}", file=sys.stderr, flush=True)
 
 
 def _run(cmd: list[str]) -> None:
@@ -92,13 +107,15 @@ def _run(cmd: list[str]) -> None:
 def build(verbose: bool = False) -> Path:
     """Compile every source and link libanima_attn.so; returns the library path."""
     cc = hipcc()
+    SGPR_SPILL_WARNINGS.clear()
     BUILD.mkdir(exist_ok=True)
     objs = []
     cmds = []
     for src in SOURCES:
         obj = BUILD / (Path(src).stem + ".o")
         objs.append(str(obj))
-        cmds.append([cc, *DEVICE_FLAGS, RESOURCE_REMARK, "-c", str(CSRC / src), "-o", str(obj)])
+        cmds.append([cc, *DEVICE_FLAGS, *SOURCE_FLAGS.get(src, []), RESOURCE_REMARK, "-c",
+                     str(CSRC / src), "-o", str(obj)])
     workers = max(1, min(len(cmds), os.cpu_count() or 1, 8))
     with ThreadPoolExecutor(workers) as pool:
         for cmd, _ in zip(cmds, pool.map(_run, cmds)):
