@@ -10,6 +10,7 @@ raises RuntimeError.
 from __future__ import annotations
 
 import ctypes
+import functools
 import threading
 from ctypes import Structure, c_char_p, c_float, c_int, c_int64, c_size_t, c_void_p
 from pathlib import Path
@@ -180,6 +181,22 @@ def dtype_code(t: torch.Tensor) -> int:
         return DTYPE_CODES[t.dtype]
     except KeyError:
         raise ValueError(f"unsupported dtype {t.dtype}: only bfloat16 is implemented") from None
+
+
+def on_device(fn):
+    """Decorator: runs fn(t, ...) with the GPU of its first argument t as the
+    current HIP device. The library reads the current device (its CU count sizes
+    the forward's split plan and grid) and launches on the stream it is given,
+    which must belong to that same device."""
+
+    @functools.wraps(fn)
+    def wrapper(t, *args, **kwargs):
+        if not t.is_cuda:  # rejected by fn's own checks
+            return fn(t, *args, **kwargs)
+        with torch.cuda.device(t.device):
+            return fn(t, *args, **kwargs)
+
+    return wrapper
 
 
 def stream(t: torch.Tensor) -> int:

@@ -21,7 +21,7 @@ import os
 import torch
 
 from . import _lib
-from .kernels.common import _check
+from .kernels.common import _check, custom_op
 
 
 @functools.cache
@@ -114,6 +114,7 @@ def _fwd_args(q, k, v, out, lse, seqused_k, ln_pad) -> _lib.AttnFwdArgs:
     return a
 
 
+@_lib.on_device
 def _launch_fwd(q, k, v, *, want_lse, seqused_k=None, ln_pad=None):
     """Runs aa_attn_fwd; returns (out [B,Sq,H,hd] contiguous, lse [B,H,Sq] or None)."""
     _validate(q, k, v)
@@ -138,6 +139,7 @@ def _launch_fwd(q, k, v, *, want_lse, seqused_k=None, ln_pad=None):
     return out, lse
 
 
+@_lib.on_device
 def _launch_bwd(dout, q, k, v, out, lse):
     _validate(q, k, v)
     if dout.shape != q.shape or out.shape != q.shape:
@@ -177,7 +179,7 @@ def _launch_bwd(dout, q, k, v, out, lse):
 # --------------------------------------------------------------------- ops --
 
 
-@torch.library.custom_op("anima_flat::fa_fwd", mutates_args=())
+@custom_op("anima_flat::fa_fwd", mutates_args=())
 def _fa_fwd(
     q: torch.Tensor, k: torch.Tensor, v: torch.Tensor
 ) -> tuple[torch.Tensor, torch.Tensor]:
@@ -192,7 +194,7 @@ def _(q, k, v):
     )
 
 
-@torch.library.custom_op("anima_flat::fa_fwd_nolse", mutates_args=())
+@custom_op("anima_flat::fa_fwd_nolse", mutates_args=())
 def _fa_fwd_nolse(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
     out, _ = _launch_fwd(q, k, v, want_lse=False)
     return out
@@ -203,7 +205,7 @@ def _(q, k, v):
     return q.new_empty(q.shape)
 
 
-@torch.library.custom_op("anima_flat::fa_fwd_k", mutates_args=())
+@custom_op("anima_flat::fa_fwd_k", mutates_args=())
 def _fa_fwd_k(
     q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, seqused_k: torch.Tensor
 ) -> tuple[torch.Tensor, torch.Tensor]:
@@ -218,7 +220,7 @@ def _(q, k, v, seqused_k):
     )
 
 
-@torch.library.custom_op("anima_flat::fa_fwd_k_ctx", mutates_args=())
+@custom_op("anima_flat_amd::fa_fwd_k_ctx", mutates_args=())
 def _fa_fwd_k_ctx(
     q: torch.Tensor,
     k: torch.Tensor,
@@ -237,7 +239,7 @@ def _(q, k, v, seqused_k, ln_pad):
     return q.new_empty(q.shape)
 
 
-@torch.library.custom_op("anima_flat::fa_bwd", mutates_args=())
+@custom_op("anima_flat::fa_bwd", mutates_args=())
 def _fa_bwd(
     dout: torch.Tensor,
     q: torch.Tensor,

@@ -139,11 +139,12 @@ def context_lengths(ctx: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     ln_pad = torch.empty(B, dtype=torch.float32, device=ctx.device)
     ws_bytes = _lib.lib().aa_context_lengths_workspace(B, S)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=ctx.device)
-    _lib.check(
-        _lib.lib().aa_context_lengths(
-            ctx.data_ptr(), B, S, C, ctx.stride(0), ctx.stride(1), _ELEM_BYTES[ctx.dtype],
-            seqused.data_ptr(), ln_pad.data_ptr(), ws.data_ptr(), ws_bytes, _lib.stream(ctx),
-        ),
-        "context_lengths",
-    )
+    with torch.cuda.device(ctx.device):
+        _lib.check(
+            _lib.lib().aa_context_lengths(
+                ctx.data_ptr(), B, S, C, ctx.stride(0), ctx.stride(1), _ELEM_BYTES[ctx.dtype],
+                seqused.data_ptr(), ln_pad.data_ptr(), ws.data_ptr(), ws_bytes, _lib.stream(ctx),
+            ),
+            "context_lengths",
+        )
     return seqused, ln_pad

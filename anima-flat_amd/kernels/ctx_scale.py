@@ -15,7 +15,7 @@ from __future__ import annotations
 import torch
 
 from .. import _lib
-from .common import _check
+from .common import _check, custom_op
 
 
 def _check_hd(hd: int) -> None:
@@ -23,26 +23,27 @@ def _check_hd(hd: int) -> None:
         raise ValueError(f"head_dim {hd} is not supported (128 only)")
 
 
-@torch.library.custom_op("anima_flat::ctx_scale", mutates_args=())
+@custom_op("anima_flat::ctx_scale", mutates_args=())
 def _ctx_scale(out: torch.Tensor, lse: torch.Tensor, ln_pad: torch.Tensor) -> torch.Tensor:
     B, S, H, hd = out.shape
     _check_hd(hd)
     y = torch.empty_like(out)
-    _lib.check(
-        _lib.lib().aa_ctx_scale_fwd(
-            out.data_ptr(),
-            lse.data_ptr(),
-            ln_pad.data_ptr(),
-            y.data_ptr(),
-            B,
-            S,
-            H,
-            hd,
-            _lib.dtype_code(out),
-            _lib.stream(out),
-        ),
-        "ctx_scale",
-    )
+    with torch.cuda.device(out.device):
+        _lib.check(
+            _lib.lib().aa_ctx_scale_fwd(
+                out.data_ptr(),
+                lse.data_ptr(),
+                ln_pad.data_ptr(),
+                y.data_ptr(),
+                B,
+                S,
+                H,
+                hd,
+                _lib.dtype_code(out),
+                _lib.stream(out),
+            ),
+            "ctx_scale",
+        )
     return y
 
 
@@ -51,7 +52,7 @@ def _(out, lse, ln_pad):
     return torch.empty_like(out)
 
 
-@torch.library.custom_op("anima_flat::ctx_scale_bwd", mutates_args=())
+@custom_op("anima_flat::ctx_scale_bwd", mutates_args=())
 def _ctx_scale_bwd_op(
     out: torch.Tensor, lse: torch.Tensor, ln_pad: torch.Tensor, dy: torch.Tensor
 ) -> tuple[torch.Tensor, torch.Tensor]:
@@ -60,23 +61,24 @@ def _ctx_scale_bwd_op(
     dy = dy.contiguous()
     dout = torch.empty_like(out)
     dlse = torch.empty_like(lse)
-    _lib.check(
-        _lib.lib().aa_ctx_scale_bwd(
-            out.data_ptr(),
-            lse.data_ptr(),
-            ln_pad.data_ptr(),
-            dy.data_ptr(),
-            dout.data_ptr(),
-            dlse.data_ptr(),
-            B,
-            S,
-            H,
-            hd,
-            _lib.dtype_code(out),
-            _lib.stream(out),
-        ),
-        "ctx_scale_bwd",
-    )
+    with torch.cuda.device(out.device):
+        _lib.check(
+            _lib.lib().aa_ctx_scale_bwd(
+                out.data_ptr(),
+                lse.data_ptr(),
+                ln_pad.data_ptr(),
+                dy.data_ptr(),
+                dout.data_ptr(),
+                dlse.data_ptr(),
+                B,
+                S,
+                H,
+                hd,
+                _lib.dtype_code(out),
+                _lib.stream(out),
+            ),
+            "ctx_scale_bwd",
+        )
     return dout, dlse
 
 

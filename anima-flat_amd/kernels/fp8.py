@@ -16,24 +16,25 @@ from __future__ import annotations
 import torch
 
 from .. import _lib
-from .common import _check
+from .common import _check, custom_op
 
 FP8 = torch.float8_e4m3fn
 FP8_MAX = 448.0
 
 
-@torch.library.custom_op("anima_flat::rowquant", mutates_args=())
+@custom_op("anima_flat::rowquant", mutates_args=())
 def _rowquant(x: torch.Tensor, gelu: bool) -> tuple[torch.Tensor, torch.Tensor]:
     B, S, K = x.shape
     q = torch.empty(B, S, K, dtype=FP8, device=x.device)
     s = torch.empty(B * S, 1, dtype=torch.float32, device=x.device)
-    _lib.check(
-        _lib.lib().aa_rowquant(
-            x.data_ptr(), B * S, K, int(gelu), q.data_ptr(), s.data_ptr(), _lib.dtype_code(x),
-            _lib.stream(x),
-        ),
-        "rowquant",
-    )
+    with torch.cuda.device(x.device):
+        _lib.check(
+            _lib.lib().aa_rowquant(
+                x.data_ptr(), B * S, K, int(gelu), q.data_ptr(), s.data_ptr(), _lib.dtype_code(x),
+                _lib.stream(x),
+            ),
+            "rowquant",
+        )
     return q, s
 
 

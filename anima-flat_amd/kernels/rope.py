@@ -19,7 +19,7 @@ from __future__ import annotations
 import torch
 
 from .. import _lib
-from .common import _check
+from .common import _check, custom_op
 
 
 def _f32(t: torch.Tensor) -> torch.Tensor:
@@ -42,30 +42,31 @@ def _launch_qkv(qkv, q_weight, k_weight, cos, sin, heads, eps, with_v):
     q = qkv.new_empty((B, S, heads, hd))
     k = torch.empty_like(q)
     v = torch.empty_like(q) if with_v else None
-    _lib.check(
-        _lib.lib().aa_qkv_norm_rope_fwd(
-            qkv.data_ptr(),
-            q.data_ptr(),
-            k.data_ptr(),
-            _lib.ptr(v),
-            _f32(q_weight).data_ptr(),
-            _f32(k_weight).data_ptr(),
-            _f32(cos).data_ptr(),
-            _f32(sin).data_ptr(),
-            B,
-            S,
-            heads,
-            hd,
-            eps,
-            _lib.dtype_code(qkv),
-            _lib.stream(qkv),
-        ),
-        "qkv_norm_rope",
-    )
+    with torch.cuda.device(qkv.device):
+        _lib.check(
+            _lib.lib().aa_qkv_norm_rope_fwd(
+                qkv.data_ptr(),
+                q.data_ptr(),
+                k.data_ptr(),
+                _lib.ptr(v),
+                _f32(q_weight).data_ptr(),
+                _f32(k_weight).data_ptr(),
+                _f32(cos).data_ptr(),
+                _f32(sin).data_ptr(),
+                B,
+                S,
+                heads,
+                hd,
+                eps,
+                _lib.dtype_code(qkv),
+                _lib.stream(qkv),
+            ),
+            "qkv_norm_rope",
+        )
     return q, k, v
 
 
-@torch.library.custom_op("anima_flat::qkv_norm_rope", mutates_args=())
+@custom_op("anima_flat::qkv_norm_rope", mutates_args=())
 def _qkv_norm_rope(
     qkv: torch.Tensor,
     q_weight: torch.Tensor,
@@ -86,27 +87,28 @@ def _(qkv, q_weight, k_weight, cos, sin, heads, eps):
     return q, torch.empty_like(q)
 
 
-@torch.library.custom_op("anima_flat::head_norm", mutates_args=())
+@custom_op("anima_flat::head_norm", mutates_args=())
 def _head_norm(x: torch.Tensor, weight: torch.Tensor, heads: int, eps: float) -> torch.Tensor:
     B, S, _ = x.shape
     hd = weight.numel()
     _check_hd(hd)
     y = x.new_empty((B, S, heads, hd))
-    _lib.check(
-        _lib.lib().aa_head_norm_fwd(
-            x.data_ptr(),
-            y.data_ptr(),
-            _f32(weight).data_ptr(),
-            B,
-            S,
-            heads,
-            hd,
-            eps,
-            _lib.dtype_code(x),
-            _lib.stream(x),
-        ),
-        "head_norm",
-    )
+    with torch.cuda.device(x.device):
+        _lib.check(
+            _lib.lib().aa_head_norm_fwd(
+                x.data_ptr(),
+                y.data_ptr(),
+                _f32(weight).data_ptr(),
+                B,
+                S,
+                heads,
+                hd,
+                eps,
+                _lib.dtype_code(x),
+                _lib.stream(x),
+            ),
+            "head_norm",
+        )
     return y
 
 
@@ -127,29 +129,30 @@ def _head_norm_bwd(x, dy, weight, heads, eps):
     dw = torch.empty(hd, dtype=torch.float32, device=x.device)
     ws_bytes = _lib.lib().aa_head_norm_bwd_workspace(B, S, heads, hd)
     ws = torch.empty(max(ws_bytes // 4, 1), dtype=torch.float32, device=x.device)
-    _lib.check(
-        _lib.lib().aa_head_norm_bwd(
-            x.data_ptr(),
-            dy.data_ptr(),
-            dx.data_ptr(),
-            _f32(weight).data_ptr(),
-            dw.data_ptr(),
-            ws.data_ptr(),
-            ws_bytes,
-            B,
-            S,
-            heads,
-            hd,
-            eps,
-            _lib.dtype_code(x),
-            _lib.stream(x),
-        ),
-        "head_norm_bwd",
-    )
+    with torch.cuda.device(x.device):
+        _lib.check(
+            _lib.lib().aa_head_norm_bwd(
+                x.data_ptr(),
+                dy.data_ptr(),
+                dx.data_ptr(),
+                _f32(weight).data_ptr(),
+                dw.data_ptr(),
+                ws.data_ptr(),
+                ws_bytes,
+                B,
+                S,
+                heads,
+                hd,
+                eps,
+                _lib.dtype_code(x),
+                _lib.stream(x),
+            ),
+            "head_norm_bwd",
+        )
     return dx, dw.to(weight.dtype)
 
 
-@torch.library.custom_op("anima_flat::head_norm_bwd", mutates_args=())
+@custom_op("anima_flat::head_norm_bwd", mutates_args=())
 def _head_norm_bwd_op(
     x: torch.Tensor, dy: torch.Tensor, weight: torch.Tensor, heads: int, eps: float
 ) -> tuple[torch.Tensor, torch.Tensor]:
@@ -179,7 +182,7 @@ torch.library.register_autograd(
 )
 
 
-@torch.library.custom_op("anima_flat::qkv_norm_rope_v", mutates_args=())
+@custom_op("anima_flat::qkv_norm_rope_v", mutates_args=())
 def _qkv_norm_rope_v(
     qkv: torch.Tensor,
     q_weight: torch.Tensor,
@@ -218,35 +221,36 @@ def _qkv_norm_rope_bwd(qkv, dq, dk, dv, q_weight, k_weight, cos, sin, heads, eps
     dkw = torch.empty(hd, dtype=torch.float32, device=qkv.device)
     ws_bytes = _lib.lib().aa_qkv_norm_rope_bwd_workspace(B, S, heads, hd)
     ws = torch.empty(max(ws_bytes // 4, 1), dtype=torch.float32, device=qkv.device)
-    _lib.check(
-        _lib.lib().aa_qkv_norm_rope_bwd(
-            qkv.data_ptr(),
-            dq.data_ptr(),
-            dk.data_ptr(),
-            dv.data_ptr(),
-            dqkv.data_ptr(),
-            _f32(q_weight).data_ptr(),
-            _f32(k_weight).data_ptr(),
-            _f32(cos).data_ptr(),
-            _f32(sin).data_ptr(),
-            dqw.data_ptr(),
-            dkw.data_ptr(),
-            ws.data_ptr(),
-            ws_bytes,
-            B,
-            S,
-            heads,
-            hd,
-            eps,
-            _lib.dtype_code(qkv),
-            _lib.stream(qkv),
-        ),
-        "qkv_norm_rope_bwd",
-    )
+    with torch.cuda.device(qkv.device):
+        _lib.check(
+            _lib.lib().aa_qkv_norm_rope_bwd(
+                qkv.data_ptr(),
+                dq.data_ptr(),
+                dk.data_ptr(),
+                dv.data_ptr(),
+                dqkv.data_ptr(),
+                _f32(q_weight).data_ptr(),
+                _f32(k_weight).data_ptr(),
+                _f32(cos).data_ptr(),
+                _f32(sin).data_ptr(),
+                dqw.data_ptr(),
+                dkw.data_ptr(),
+                ws.data_ptr(),
+                ws_bytes,
+                B,
+                S,
+                heads,
+                hd,
+                eps,
+                _lib.dtype_code(qkv),
+                _lib.stream(qkv),
+            ),
+            "qkv_norm_rope_bwd",
+        )
     return dqkv, dqw.to(q_weight.dtype), dkw.to(k_weight.dtype)
 
 
-@torch.library.custom_op("anima_flat::qkv_norm_rope_bwd", mutates_args=())
+@custom_op("anima_flat::qkv_norm_rope_bwd", mutates_args=())
 def _qkv_norm_rope_bwd_op(
     qkv: torch.Tensor,
     dq: torch.Tensor,
@@ -331,84 +335,6 @@ def qkv_norm_rope(qkv, q_weight, k_weight, cos, sin, heads, eps=1e-5):
     B, S, _ = qkv.shape
     v = qkv.view(B, S, 3, heads, 2 * cos.shape[1])[:, :, 2]
     return q, k, v
-
-
-@torch.library.custom_op("anima_flat::qkv_proj_norm_rope", mutates_args=())
-def _qkv_proj_norm_rope(
-    hid: torch.Tensor,
-    weight: torch.Tensor,
-    q_weight: torch.Tensor,
-    k_weight: torch.Tensor,
-    cos: torch.Tensor,
-    sin: torch.Tensor,
-    heads: int,
-    eps: float,
-) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    B, S, D = hid.shape
-    hd = 2 * cos.shape[1]
-    q = hid.new_empty((B, S, heads, hd))
-    k = torch.empty_like(q)
-    v = torch.empty_like(q)
-    _lib.check(
-        _lib.lib().aa_qkv_proj_norm_rope(
-            hid.data_ptr(),
-            hid.stride(1),
-            weight.data_ptr(),
-            q.data_ptr(),
-            k.data_ptr(),
-            v.data_ptr(),
-            _f32(q_weight).data_ptr(),
-            _f32(k_weight).data_ptr(),
-            _f32(cos).data_ptr(),
-            _f32(sin).data_ptr(),
-            B,
-            S,
-            heads,
-            hd,
-            eps,
-            _lib.dtype_code(hid),
-            _lib.stream(hid),
-        ),
-        "qkv_proj_norm_rope",
-    )
-    return q, k, v
-
-
-@_qkv_proj_norm_rope.register_fake
-def _(hid, weight, q_weight, k_weight, cos, sin, heads, eps):
-    B, S, _ = hid.shape
-    q = hid.new_empty((B, S, heads, 2 * cos.shape[1]))
-    return q, torch.empty_like(q), torch.empty_like(q)
-
-
-def qkv_proj_norm_rope(hid, weight, q_weight, k_weight, cos, sin, heads, eps=1e-5):
-    """`qkv_norm_rope(F.linear(hid, weight), ...)` as one kernel (the block's
-    `b.qkv` projection followed by the prologue, src/model.py:308-316), with the
-    projection output kept on chip. Inference only (no autograd).
-
-    Args:
-        hid: `[B, S, heads * head_dim]` bf16; rows may be strided (last-dim stride 1).
-        weight: `[3 * heads * head_dim, heads * head_dim]` bf16, contiguous (nn.Linear, no bias).
-        q_weight, k_weight, cos, sin, heads, eps: as for `qkv_norm_rope`.
-
-    Returns:
-        `(q, k, v)`, each a contiguous `[B, S, heads, head_dim]`.
-    """
-    _check(hid, weight, q_weight, k_weight, cos, sin)
-    hd = 2 * cos.shape[1]
-    D = heads * hd
-    if hid.ndim != 3 or hid.shape[-1] != D or hid.stride(-1) != 1 or hid.stride(0) != hid.shape[1] * hid.stride(1):
-        raise ValueError("hid must be [B, S, heads * head_dim] with unit last-dim stride and uniform rows")
-    if not weight.is_contiguous() or tuple(weight.shape) != (3 * D, D) or weight.dtype != hid.dtype:
-        raise ValueError("weight must be a contiguous [3 * heads * head_dim, heads * head_dim] matrix of hid's dtype")
-    if cos.shape != sin.shape or cos.shape[0] != hid.shape[1] or (cos.shape[1] & (cos.shape[1] - 1)):
-        raise ValueError("cos/sin must be [S, head_dim // 2] with a power-of-two width")
-    _check_hd(hd)
-    if torch.is_grad_enabled() and (hid.requires_grad or weight.requires_grad or q_weight.requires_grad):
-        raise RuntimeError("qkv_proj_norm_rope has no backward: use F.linear + qkv_norm_rope for training")
-    return _qkv_proj_norm_rope(
-        hid, weight, q_weight.contiguous(), k_weight.contiguous(), cos.contiguous(), sin.contiguous(), heads, eps
-    )
 
 
 def head_norm(x, weight, heads, eps=1e-5):

@@ -41,6 +41,22 @@ def pkg():
 
 
 @pytest.fixture(scope="session")
+def fp8(pkg):
+    """The opt-in rowquant module (anima_flat_amd.kernels.fp8)."""
+    import importlib
+
+    return importlib.import_module("anima_flat_amd.kernels.fp8")
+
+
+@pytest.fixture(scope="session")
+def proj(pkg):
+    """The opt-in fused-projection module (anima_flat_amd.kernels.proj)."""
+    import importlib
+
+    return importlib.import_module("anima_flat_amd.kernels.proj")
+
+
+@pytest.fixture(scope="session")
 def dev():
     return torch.device("cuda:0")
 

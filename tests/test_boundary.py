@@ -134,7 +134,7 @@ def test_invalid_arguments_fail_before_any_launch(pkg, lib):
         L.check(L.AA_EHIP, "x")
 
 
-def test_cpu_tensors_are_rejected(pkg):
+def test_cpu_tensors_are_rejected(pkg, fp8, proj):
     q = torch.zeros(1, 4, 1, 128, dtype=torch.bfloat16)
     with pytest.raises(ValueError, match="CUDA tensors required"):
         pkg.attention(q, q, q)
@@ -152,22 +152,82 @@ def test_cpu_tensors_are_rejected(pkg):
     with pytest.raises(ValueError, match="CUDA tensors required"):
         pkg.context_lengths(torch.zeros(1, 4, 8, dtype=torch.bfloat16))
     with pytest.raises(ValueError, match="CUDA tensors required"):
-        pkg.rowquant(torch.zeros(1, 4, 8, dtype=torch.bfloat16))
+        fp8.rowquant(torch.zeros(1, 4, 8, dtype=torch.bfloat16))
     with pytest.raises(ValueError, match="CUDA"):
-        pkg.qkv_proj_norm_rope(torch.zeros(1, 4, 256, dtype=torch.bfloat16),
+        proj.qkv_proj_norm_rope(torch.zeros(1, 4, 256, dtype=torch.bfloat16),
                                torch.zeros(768, 256, dtype=torch.bfloat16), torch.ones(128),
                                torch.ones(128), torch.zeros(4, 64), torch.zeros(4, 64), 2)
     assert pkg.use_fa4(q) is False
 
 
-def test_ops_are_registered_with_reference_names(pkg):
+def test_ops_are_registered_with_reference_names(pkg, fp8, proj):
     for name in ("fa_fwd", "fa_fwd_nolse", "fa_fwd_k", "fa_bwd", "qkv_norm_rope", "qkv_norm_rope_v",
                  "qkv_norm_rope_bwd", "head_norm", "head_norm_bwd", "ctx_scale", "ctx_scale_bwd",
-                 "rowquant", "qkv_proj_norm_rope"):
+                 "rowquant"):
         assert hasattr(torch.ops.anima_flat, name), name
+    # Ops with no counterpart in the reference live in their own namespace.
+    for name in ("fa_fwd_k_ctx", "qkv_proj_norm_rope"):
+        assert hasattr(torch.ops.anima_flat_amd, name), name
+        assert not hasattr(torch.ops.anima_flat, name), name
 
 
-def test_fake_shapes_on_meta_tensors(pkg):
+_STUB = """
+import sys, torch
+sys.path.insert(0, {root!r})
+
+@torch.library.custom_op("anima_flat::{name}", mutates_args=())
+def stub(x: torch.Tensor, flag: bool) -> tuple[torch.Tensor, torch.Tensor]:
+    return x.clone().fill_(7.0), x.new_zeros(1)
+
+import __graft_entry__
+"""
+
+
+def _run_py(code: str) -> subprocess.CompletedProcess:
+    return subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=300,
+                          cwd=ROOT)
+
+
+def test_package_leaves_foreign_rowquant_alone():
+    """The reference's src/kernels/fp8.py registers anima_flat::rowquant; importing this
+    package must not replace it, and importing the opt-in module must raise, not re-bind."""
+    code = _STUB.format(root=str(ROOT), name="rowquant") + """
+amd = __graft_entry__.load_package()
+assert not hasattr(amd, "rowquant")
+x = torch.zeros(2, 3)
+assert torch.equal(torch.ops.anima_flat.rowquant(x, False)[0], torch.full((2, 3), 7.0))
+try:
+    import anima_flat_amd.kernels.fp8  # noqa: F401
+except RuntimeError as e:
+    assert "anima_flat::rowquant is already registered" in str(e), e
+else:
+    raise AssertionError("second registration of anima_flat::rowquant did not raise")
+assert torch.equal(torch.ops.anima_flat.rowquant(x, False)[0], torch.full((2, 3), 7.0))
+print("ok")
+"""
+    r = _run_py(code)
+    assert r.returncode == 0 and r.stdout.strip().endswith("ok"), r.stdout + r.stderr
+
+
+def test_package_refuses_to_rebind_reference_attention_op():
+    """With the reference's src/attention.py imported first (anima_flat::fa_fwd registered),
+    importing the package raises instead of silently taking the name over."""
+    code = _STUB.format(root=str(ROOT), name="fa_fwd") + """
+try:
+    __graft_entry__.load_package()
+except RuntimeError as e:
+    assert "anima_flat::fa_fwd is already registered" in str(e), e
+else:
+    raise AssertionError("package import re-bound anima_flat::fa_fwd")
+x = torch.zeros(2, 3)
+assert torch.equal(torch.ops.anima_flat.fa_fwd(x, False)[0], torch.full((2, 3), 7.0))
+print("ok")
+"""
+    r = _run_py(code)
+    assert r.returncode == 0 and r.stdout.strip().endswith("ok"), r.stdout + r.stderr
+
+
+def test_fake_shapes_on_meta_tensors(pkg, fp8, proj):
     B, Sq, Sk, H = 2, 40, 24, 3
     q = torch.empty(B, Sq, H, 128, dtype=torch.bfloat16, device="meta")
     k = torch.empty(B, Sk, H, 128, dtype=torch.bfloat16, device="meta")
@@ -195,7 +255,7 @@ def test_fake_shapes_on_meta_tensors(pkg):
     assert qx.shape == x.shape and qx.dtype == torch.float8_e4m3fn and sx.shape == (B * Sq, 1)
     hid = torch.empty(B, Sq, H * 128, dtype=torch.bfloat16, device="meta")
     wq = torch.empty(3 * H * 128, H * 128, dtype=torch.bfloat16, device="meta")
-    outs = torch.ops.anima_flat.qkv_proj_norm_rope(hid, wq, w, w, cos, cos, H, 1e-6)
+    outs = torch.ops.anima_flat_amd.qkv_proj_norm_rope(hid, wq, w, w, cos, cos, H, 1e-6)
     assert all(t.shape == (B, Sq, H, 128) and t.dtype == torch.bfloat16 for t in outs)
 
 

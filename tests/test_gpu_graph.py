@@ -18,7 +18,7 @@ pytestmark = pytest.mark.gpu
 BF = torch.bfloat16
 
 
-def test_graph_replays_match_eager(pkg):
+def test_graph_replays_match_eager(pkg, fp8, proj):
     dev = torch.device("cuda:0")
     B, S, H, d = 2, 512, 4, 128
     inp = ref.prologue_inputs(B, S, H, d, seed=77)
@@ -42,8 +42,8 @@ def test_graph_replays_match_eager(pkg):
         qx = pkg.head_norm(x, w, H, 1e-6)
         seq, lnp = pkg.context_lengths(ctx)
         o_cross = pkg.cross_attention_trimmed(qx, kc, vc, seq, lnp)
-        oq, os_ = pkg.rowquant(o_self)
-        pq, pk, pv = pkg.qkv_proj_norm_rope(hid, wqkv, qw, kw, cos, sin, H, 1e-6)
+        oq, os_ = fp8.rowquant(o_self)
+        pq, pk, pv = proj.qkv_proj_norm_rope(hid, wqkv, qw, kw, cos, sin, H, 1e-6)
         return [o_self, o_cross, oq.view(torch.uint8), os_, seq, lnp, pq, pk, pv]
 
     with torch.no_grad():

@@ -37,9 +37,9 @@ def _inputs(B, S, H, seed, rope_scale=(1.0, 1.0)):
     return hid, w, qw, kw, cos[:S].contiguous(), sin[:S].contiguous()
 
 
-def _run(pkg, hid, w, qw, kw, cos, sin, H, eps, dev="cuda:0"):
+def _run(proj, hid, w, qw, kw, cos, sin, H, eps, dev="cuda:0"):
     with torch.no_grad():
-        out = pkg.qkv_proj_norm_rope(
+        out = proj.qkv_proj_norm_rope(
             hid.to(dev, BF), w.to(dev, BF), qw.to(dev), kw.to(dev), cos.to(dev), sin.to(dev), H, eps
         )
     torch.cuda.synchronize()
@@ -65,14 +65,14 @@ def _check(outs, exps, tag):
         (3, 5, 1, 1e-6, (1.0, 1.0)),
     ],
 )
-def test_qkv_proj_matches_oracle(pkg, B, S, H, eps, scale):
+def test_qkv_proj_matches_oracle(pkg, proj, B, S, H, eps, scale):
     hid, w, qw, kw, cos, sin = _inputs(B, S, H, seed=900 + S + H, rope_scale=scale)
-    outs = _run(pkg, hid, w, qw, kw, cos, sin, H, eps)
+    outs = _run(proj, hid, w, qw, kw, cos, sin, H, eps)
     exps = ref.qkv_proj_norm_rope(hid, w, qw, kw, cos, sin, H, eps)
     _check(outs, exps, f"B{B} S{S} H{H}")
 
 
-def test_qkv_proj_strided_rows_and_equals_unfused_path(pkg):
+def test_qkv_proj_strided_rows_and_equals_unfused_path(pkg, proj):
     """hid as a strided view (row stride 2560 > 2048); the fused result equals
     F.linear + qkv_norm_rope on the GPU to the same bar."""
     B, S, H = 2, 512, 16
@@ -81,7 +81,7 @@ def test_qkv_proj_strided_rows_and_equals_unfused_path(pkg):
     wide[:, :, 256:2304] = hid
     dev = "cuda:0"
     view = wide.to(dev)[:, :, 256:2304]
-    outs = _run(pkg, view, w, qw, kw, cos, sin, H, 1e-6)
+    outs = _run(proj, view, w, qw, kw, cos, sin, H, 1e-6)
     exps = ref.qkv_proj_norm_rope(hid, w, qw, kw, cos, sin, H, 1e-6)
     _check(outs, exps, "strided")
     with torch.no_grad():
@@ -93,23 +93,23 @@ def test_qkv_proj_strided_rows_and_equals_unfused_path(pkg):
         parity(a, e.float().cpu(), max_abs=bar, name=f"fused vs unfused {name}")
 
 
-def test_qkv_proj_rejects_bad_inputs(pkg):
+def test_qkv_proj_rejects_bad_inputs(pkg, proj):
     dev = "cuda:0"
     hid = torch.zeros(1, 8, 256, dtype=BF, device=dev)
     w = torch.zeros(768, 256, dtype=BF, device=dev)
     qw = torch.ones(128, device=dev)
     cs = torch.zeros(8, 64, device=dev)
     with pytest.raises(ValueError, match="weight"):
-        pkg.qkv_proj_norm_rope(hid, w[:, :128], qw, qw, cs, cs, 2)
+        proj.qkv_proj_norm_rope(hid, w[:, :128], qw, qw, cs, cs, 2)
     with pytest.raises(ValueError, match="hid"):
-        pkg.qkv_proj_norm_rope(hid[:, :, :128], w, qw, qw, cs, cs, 2)
+        proj.qkv_proj_norm_rope(hid[:, :, :128], w, qw, qw, cs, cs, 2)
     with pytest.raises(RuntimeError, match="backward"):
-        pkg.qkv_proj_norm_rope(hid.clone().requires_grad_(True), w, qw, qw, cs, cs, 2)
+        proj.qkv_proj_norm_rope(hid.clone().requires_grad_(True), w, qw, qw, cs, cs, 2)
 
 
-def test_qkv_proj_deterministic(pkg):
+def test_qkv_proj_deterministic(pkg, proj):
     hid, w, qw, kw, cos, sin = _inputs(1, 700, 16, seed=31)
-    a = _run(pkg, hid, w, qw, kw, cos, sin, 16, 1e-6)
-    b = _run(pkg, hid, w, qw, kw, cos, sin, 16, 1e-6)
+    a = _run(proj, hid, w, qw, kw, cos, sin, 16, 1e-6)
+    b = _run(proj, hid, w, qw, kw, cos, sin, 16, 1e-6)
     for x, y in zip(a, b):
         assert torch.equal(x, y)

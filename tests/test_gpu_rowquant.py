@@ -34,10 +34,10 @@ def _rows(B, S, K, seed, spread=False):
         (1, 7, 1000, True),  # K not a multiple of 256 * 8
     ],
 )
-def test_rowquant_bit_exact(pkg, B, S, K, spread):
+def test_rowquant_bit_exact(pkg, fp8, B, S, K, spread):
     x = _rows(B, S, K, seed=B * 31 + S + K, spread=spread)
     x[0, 0] = 0.0  # an all-zero row: scale 1e-12 / 448, bytes 0
-    q, s = pkg.rowquant(x.to("cuda:0"))
+    q, s = fp8.rowquant(x.to("cuda:0"))
     torch.cuda.synchronize()
     eq, es = ref.rowquant(x)
     assert q.dtype == torch.float8_e4m3fn and q.shape == x.shape and s.shape == (B * S, 1)
@@ -46,10 +46,10 @@ def test_rowquant_bit_exact(pkg, B, S, K, spread):
     assert torch.equal(qb, eb), f"{(qb != eb).sum().item()} bytes differ"
 
 
-def test_rowquant_gelu(pkg):
+def test_rowquant_gelu(pkg, fp8):
     B, S, K = 2, 48, 8192
     x = _rows(B, S, K, seed=9) * 3
-    q, s = pkg.rowquant(x.to("cuda:0"), gelu=True)
+    q, s = fp8.rowquant(x.to("cuda:0"), gelu=True)
     torch.cuda.synchronize()
     eq, es = ref.rowquant(x, gelu=True)
     torch.testing.assert_close(s.cpu(), es, rtol=4e-7, atol=0)
@@ -60,18 +60,18 @@ def test_rowquant_gelu(pkg):
     assert ((a - e).abs() <= e.abs() * 0.1251 + 2.0**-9).all()
 
 
-def test_rowquant_of_attention_output(pkg):
+def test_rowquant_of_attention_output(pkg, fp8):
     """rowquant(attention(...)) as the model's FP8 path calls it (model.py:446)."""
     g = torch.Generator().manual_seed(13)
     q, k, v = (ref.bf16_normal((1, 256, 16, 128), g) for _ in range(3))
     out = pkg.attention(*(t.to("cuda:0", torch.bfloat16) for t in (q, k, v)))
-    oq, os_ = pkg.rowquant(out)
+    oq, os_ = fp8.rowquant(out)
     torch.cuda.synchronize()
     eq, es = ref.rowquant(out.cpu())
     assert torch.equal(os_.cpu(), es) and torch.equal(oq.cpu().view(torch.uint8), eq.view(torch.uint8))
 
 
-def test_rowquant_every_e4m3_tie_point(pkg):
+def test_rowquant_every_e4m3_tie_point(pkg, fp8):
     """Every rounding boundary of e4m3fn: each tie point between adjacent codes and its
     neighbouring fp32 values, both signs, through the kernel with scale exactly 1 (each row
     holds 448). Inputs are bf16, so the tie points are exact and the neighbours are the
@@ -91,7 +91,7 @@ def test_rowquant_every_e4m3_tie_point(pkg):
     x[:n] = vals
     x = torch.cat([torch.full((rows, 1), 448.0, dtype=torch.bfloat16), x.view(rows, K - 1)], 1)
     x = x.view(1, rows, K)
-    q, s = pkg.rowquant(x.to("cuda:0"))
+    q, s = fp8.rowquant(x.to("cuda:0"))
     torch.cuda.synchronize()
     eq, es = ref.rowquant(x)
     assert (es == 1.0).all() and torch.equal(s.cpu(), es)
