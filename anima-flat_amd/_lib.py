@@ -54,6 +54,7 @@ _PROTOTYPES: dict[str, tuple[object, list[object]]] = {
         [c_void_p] * 5 + [c_void_p, c_size_t] + [_I64] * 4 + [c_float, c_int, c_void_p],
     ),
     "aa_attn_fwd": (c_int, [c_void_p, c_void_p]),
+    "aa_attn_fwd_noalloc": (c_int, [c_void_p, c_void_p]),
     "aa_attn_fwd_workspace": (c_size_t, [_I64] * 5),
     "aa_attn_bwd_workspace": (c_size_t, [_I64] * 5),
     "aa_attn_bwd": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p]),

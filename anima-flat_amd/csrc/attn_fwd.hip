@@ -51,6 +51,8 @@
 #include <atomic>
 #include <cmath>
 #include <cstdlib>
+#include <mutex>
+#include <string>
 #include <type_traits>
 
 #include "tile_io.h"
@@ -649,6 +651,62 @@ static int prepare(const aa_attn_fwd_args* a, FwdParams& p) {
   p.part_o = (float*)a->workspace;
   p.part_lse = p.part_o + (size_t)sp.split_items * sp.nsplit * kQPerWg * kD;
   return AA_OK;
+}
+
+// Split partials of aa_attn_fwd_noalloc. split_plan splits at most ncu / 2
+// items into at most ncu / items key ranges, so the partials never exceed
+// ncu * kQPerWg * (kD + 1) floats; the array holds that for 256 CUs
+// (MI355X): 33,816,576 bytes, resident on every device the library runs on.
+constexpr size_t kFwdScratchBytes = (size_t)256 * kQPerWg * (kD + 1) * sizeof(float);
+static __device__ __align__(256) uint8_t scratch[kFwdScratchBytes];
+
+// Device address of `scratch` on the current device, looked up once per
+// device. In host code `scratch` names a host-side stand-in, so only this
+// address may be passed to kernels.
+static int fwd_scratch(void** out) {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<void*> addr[kMaxDevices];
+  static std::mutex lock;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(AA_EHIP, "attn_fwd_noalloc: no current device");
+  void* p = addr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> g(lock);
+    p = addr[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || !p)
+        return fail(AA_EHIP, std::string("attn_fwd_noalloc: hipGetSymbolAddress: ") +
+                                 hipGetErrorString(e));
+      addr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return AA_OK;
+}
+
+extern "C" int aa_attn_fwd(const aa_attn_fwd_args* a, void* stream);
+
+extern "C" int aa_attn_fwd_noalloc(const aa_attn_fwd_args* a, void* stream) {
+  clear_error();
+  if (!a) return fail(AA_EINVAL, "attn_fwd_noalloc: null args");
+  aa_attn_fwd_args b = *a;
+  b.workspace = nullptr;
+  b.workspace_bytes = 0;
+  if (a->B > 0 && a->Sq > 0 && a->Sk > 0 && a->H > 0) {
+    const size_t need =
+        split_workspace_bytes(split_plan(work_items(a->B, a->Sq, a->H), a->Sk, device_cu_count()));
+    if (need > kFwdScratchBytes)
+      return fail(AA_EUNSUPPORTED, "attn_fwd_noalloc: split partials of " + std::to_string(need) +
+                                       " bytes exceed the fixed scratch of " +
+                                       std::to_string(kFwdScratchBytes) + " bytes");
+    if (need > 0) {
+      if (int rc = fwd_scratch(&b.workspace)) return rc;
+      b.workspace_bytes = kFwdScratchBytes;
+    }
+  }
+  return aa_attn_fwd(&b, stream);
 }
 
 extern "C" int aa_attn_fwd(const aa_attn_fwd_args* a, void* stream) {

@@ -184,6 +184,20 @@ size_t aa_attn_fwd_workspace(int64_t B, int64_t Sq, int64_t Sk, int64_t H, int64
  */
 int aa_attn_fwd(const aa_attn_fwd_args* args, void* stream);
 
+/*
+ * aa_attn_fwd without a caller workspace and without any allocation: the
+ * split partials go to a fixed device array of 33,816,576 bytes that the
+ * library holds on each device it runs on until the process ends (every
+ * forward on a 256-CU device fits; a plan that needs more returns
+ * AA_EUNSUPPORTED). args->workspace / workspace_bytes are ignored. Calls on
+ * one device share that array: calls that overlap on one device (two streams
+ * at once) race and must be serialised by the caller. Same results as
+ * aa_attn_fwd (same kernels). No counterpart in the reference: for callers
+ * that cannot allocate device memory (code under HIP graph capture, serving
+ * loops, harnesses that forbid hipMalloc).
+ */
+int aa_attn_fwd_noalloc(const aa_attn_fwd_args* args, void* stream);
+
 typedef struct aa_attn_bwd_args {
   const void* dout;     /* [B, Sq, H, hd] */
   const void* q;
