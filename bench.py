@@ -121,6 +121,68 @@ def kernel_only_timer(pkg, q, k, v):
     return attn, out
 
 
+def copy_calibration(dev) -> None:
+    """One plain 256 MiB device copy (known bytes: 256 MiB read, 256 MiB written),
+    the reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes."""
+    src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+
+
+PROFILE_CASES = ("self_cfg2", "self_cfg1", "prologue_cfg2", "head_norm_cfg3", "cross_cfg3",
+                 "cross_b2_512", "rowquant_cfg3", "prologue_bwd_cfg5")
+
+
+def profile_case(name: str, steps: int, pkg, fp8, dev) -> dict:
+    """Runs one workload `steps` times and nothing else, so that a rocprofv3 run
+    (kernel trace or PMC counters) of `bench.py --profile-case NAME` sees only its
+    kernels. Inputs are the ones the headline and extras use (same shapes and seeds)."""
+    B, S, H, d, eps = 1, 4096, 16, 128, 1e-6
+    g = torch.Generator().manual_seed(1003)
+    if name in ("self_cfg2", "self_cfg1", "prologue_cfg2", "prologue_bwd_cfg5"):
+        Sx, seed = (1024, 1001) if name == "self_cfg1" else (S, 1002)
+        p = prologue_qkv(pkg, B, Sx, H, seed, dev)
+        pro = lambda: pkg.qkv_norm_rope(p["qkv"], p["q_weight"], p["k_weight"], p["cos"], p["sin"], H, eps)
+        with torch.no_grad():
+            q, k, v = pro()
+        if name == "prologue_cfg2":
+            fn = pro
+        elif name == "prologue_bwd_cfg5":
+            gq, gk, gv = (torch.randn(B, S, H, d, device=dev, dtype=BF) for _ in range(3))
+            fn = lambda: torch.ops.anima_flat.qkv_norm_rope_bwd(
+                p["qkv"], gq, gk, gv, p["q_weight"], p["k_weight"], p["cos"], p["sin"], H, eps)
+        else:
+            fn = lambda: torch.ops.anima_flat.fa_fwd_nolse(q, k, v)
+    elif name in ("head_norm_cfg3", "cross_cfg3", "cross_b2_512", "rowquant_cfg3"):
+        lens = torch.randint(32, 513, (2,), generator=g, dtype=torch.int32)
+        x = torch.randn(2, S, H * d, generator=g).to(dev, BF)
+        w = (1 + 0.02 * torch.randn(d, generator=g)).to(dev)
+        kc = torch.randn(2, 512, H, d, generator=g).to(dev, BF)
+        vc = torch.randn(2, 512, H, d, generator=g).to(dev, BF)
+        lens_d = lens.to(dev)
+        with torch.no_grad():
+            qc = pkg.head_norm(x, w, H, eps)
+        if name == "head_norm_cfg3":
+            fn = lambda: pkg.head_norm(x, w, H, eps)
+        elif name == "cross_cfg3":
+            fn = lambda: torch.ops.anima_flat.fa_fwd_k(qc, kc, vc, lens_d)
+        elif name == "cross_b2_512":
+            fn = lambda: torch.ops.anima_flat.fa_fwd_nolse(qc, kc, vc)
+        else:
+            o_att = torch.randn(2, S, H * d, generator=g).to(dev, BF)
+            fn = lambda: fp8.rowquant(o_att)
+    else:
+        raise SystemExit(f"bench.py: unknown --profile-case {name!r} (one of {', '.join(PROFILE_CASES)})")
+    with torch.no_grad():
+        for _ in range(steps):
+            fn()
+    torch.cuda.synchronize()
+    return {"profile_case": name, "steps": steps}
+
+
 def pmc_traffic(name: str):
     """HBM bytes per launch from a committed rocprofv3 PMC summary (profiles/<name>),
     line 'traffic_bytes_per_launch: N'; None when absent."""
@@ -187,6 +249,12 @@ def main() -> int:
         "forward + backward (a short run for profiling the backward kernels)",
     )
     ap.add_argument(
+        "--profile-case",
+        choices=PROFILE_CASES,
+        help="run only this workload --steps times (for rocprofv3 kernel traces and PMC passes) "
+        "and print one JSON line naming it; no timing",
+    )
+    ap.add_argument(
         "--copy-calibration",
         action="store_true",
         help="also run one plain 256 MiB device copy (known bytes) so rocprofv3 FETCH_SIZE/"
@@ -206,6 +274,11 @@ def main() -> int:
     proj = importlib.import_module("anima_flat_amd.kernels.proj")
     dev = torch.device("cuda:0")
     torch.manual_seed(0)
+    if args.profile_case:
+        if args.copy_calibration:
+            copy_calibration(dev)
+        print(json.dumps(profile_case(args.profile_case, args.steps, pkg, fp8, dev)))
+        return 0
     B, S, H, d = 1, 4096, 16, 128
     eps = 1e-6
 
@@ -220,12 +293,7 @@ def main() -> int:
         fwd = torch.ops.anima_flat.fa_fwd_nolse
         wall_ms, dev_ms = time_launches(lambda: fwd(q, k, v), args.steps, args.warmup)
     if args.copy_calibration:
-        src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
-        dst = torch.empty_like(src)
-        torch.cuda.synchronize()
-        dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
+        copy_calibration(dev)
     flops = attn_flops(B, H, S, S, d)
     value = flops / (wall_ms * 1e-3) / 1e12
     achieved = flops / (attn_ms * 1e-3) / 1e12
