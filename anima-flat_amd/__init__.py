@@ -7,6 +7,8 @@ Drop-in modules, same public signatures as the reference:
   kernels.ctx_scale <- src/kernels/ctx_scale.py (ctx_scale and its ops)
   context        <- src/model.py:51-119, 247-254 (rope_tables, Context, context trimming,
                                             context_lengths: the trim's lengths on the device)
+  vae            <- the `_attend` of src/vae.py:10-13, 239 (attend: the VAE mid-block attention,
+                                            head_dim 384; op anima_flat_amd::attend_d384)
 
 Opt-in modules, not imported here (import them explicitly):
   kernels.fp8    <- rowquant of src/kernels/fp8.py (op anima_flat::rowquant: FP8 per-token
@@ -24,7 +26,7 @@ All compute runs in libanima_attn.so (csrc/, C ABI in include/anima_attn.h),
 loaded through ctypes by _lib.py. There is no CPU or SDPA fallback.
 """
 
-from . import _lib  # noqa: F401
+from . import _lib, vae  # noqa: F401
 from .attention import attention, cross_attention_trimmed, use_fa4  # noqa: F401
 from .context import Context, context_lengths, rope_tables, trim_context  # noqa: F401
 from .kernels.ctx_scale import ctx_scale  # noqa: F401

@@ -79,7 +79,7 @@ def _prep(t: torch.Tensor) -> torch.Tensor:
     return t
 
 
-def _validate(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
+def _validate(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, head_dims=(128,)) -> None:
     if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
         raise ValueError("q, k, v must be [B, S, H, hd]")
     if k.shape != v.shape:
@@ -93,8 +93,8 @@ def _validate(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
     if not (q.device == k.device == v.device):
         raise ValueError("q, k, v must be on one device")
     _lib.dtype_code(q)
-    if q.shape[3] != 128:
-        raise ValueError(f"head_dim {q.shape[3]} is not supported (128 only)")
+    if q.shape[3] not in head_dims:
+        raise ValueError(f"head_dim {q.shape[3]} is not supported ({' or '.join(map(str, head_dims))} only)")
 
 
 def _fwd_args(q, k, v, out, lse, seqused_k, ln_pad) -> _lib.AttnFwdArgs:
@@ -115,9 +115,9 @@ def _fwd_args(q, k, v, out, lse, seqused_k, ln_pad) -> _lib.AttnFwdArgs:
 
 
 @_lib.on_device
-def _launch_fwd(q, k, v, *, want_lse, seqused_k=None, ln_pad=None):
+def _launch_fwd(q, k, v, *, want_lse, seqused_k=None, ln_pad=None, head_dims=(128,)):
     """Runs aa_attn_fwd; returns (out [B,Sq,H,hd] contiguous, lse [B,H,Sq] or None)."""
-    _validate(q, k, v)
+    _validate(q, k, v, head_dims)
     q, k, v = _prep(q), _prep(k), _prep(v)
     B, Sq, H, _ = q.shape
     out = torch.empty(q.shape, dtype=q.dtype, device=q.device)

@@ -55,6 +55,7 @@
 #include <string>
 #include <type_traits>
 
+#include "attn_fwd_d384.h"
 #include "tile_io.h"
 
 namespace aa {
@@ -590,7 +591,7 @@ static int64_t work_items(int64_t B, int64_t Sq, int64_t H) {
 }
 
 extern "C" size_t aa_attn_fwd_workspace(int64_t B, int64_t Sq, int64_t Sk, int64_t H, int64_t hd) {
-  (void)hd;
+  if (hd == 384) return attn_fwd_d384_workspace(B, Sq, Sk, H, device_cu_count());
   if (B <= 0 || Sq <= 0 || Sk <= 0 || H <= 0) return 0;
   return split_workspace_bytes(split_plan(work_items(B, Sq, H), Sk, device_cu_count()));
 }
@@ -599,7 +600,7 @@ extern "C" size_t aa_attn_fwd_workspace(int64_t B, int64_t Sq, int64_t Sk, int64
 static int prepare(const aa_attn_fwd_args* a, FwdParams& p) {
   if (!a) return fail(AA_EINVAL, "attn_fwd: null args");
   if (a->dtype != AA_DTYPE_BF16) return fail(AA_EUNSUPPORTED, "only bf16 attention is implemented");
-  if (a->hd != kD) return fail(AA_EUNSUPPORTED, "head_dim must be 128");
+  if (a->hd != kD) return fail(AA_EUNSUPPORTED, "head_dim must be 128 or 384");
   if (a->B < 0 || a->Sq < 0 || a->Sk < 0 || a->H <= 0)
     return fail(AA_EINVAL, "attn_fwd: negative size");
   if (a->Sq > (1 << 30) || a->Sk > (1 << 30) || a->H > 65535 || a->B > 65535)
@@ -655,9 +656,11 @@ static int prepare(const aa_attn_fwd_args* a, FwdParams& p) {
 
 // Split partials of aa_attn_fwd_noalloc. split_plan splits at most ncu / 2
 // items into at most ncu / items key ranges, so the partials never exceed
-// ncu * kQPerWg * (kD + 1) floats; the array holds that for 256 CUs
-// (MI355X): 33,816,576 bytes, resident on every device the library runs on.
-constexpr size_t kFwdScratchBytes = (size_t)256 * kQPerWg * (kD + 1) * sizeof(float);
+// ncu * kQPerWg * (kD + 1) floats (33,816,576 bytes at 256 CUs); the
+// head-dim-384 forward's never exceed kD384MaxPartialBytes (50,462,720). The
+// array holds the larger, resident on every device the library runs on.
+constexpr size_t kFwdScratchBytes =
+    std::max((size_t)256 * kQPerWg * (kD + 1) * sizeof(float), kD384MaxPartialBytes);
 static __device__ __align__(256) uint8_t scratch[kFwdScratchBytes];
 
 // Device address of `scratch` on the current device, looked up once per
@@ -695,8 +698,7 @@ extern "C" int aa_attn_fwd_noalloc(const aa_attn_fwd_args* a, void* stream) {
   b.workspace = nullptr;
   b.workspace_bytes = 0;
   if (a->B > 0 && a->Sq > 0 && a->Sk > 0 && a->H > 0) {
-    const size_t need =
-        split_workspace_bytes(split_plan(work_items(a->B, a->Sq, a->H), a->Sk, device_cu_count()));
+    const size_t need = aa_attn_fwd_workspace(a->B, a->Sq, a->Sk, a->H, a->hd);
     if (need > kFwdScratchBytes)
       return fail(AA_EUNSUPPORTED, "attn_fwd_noalloc: split partials of " + std::to_string(need) +
                                        " bytes exceed the fixed scratch of " +
@@ -711,6 +713,10 @@ extern "C" int aa_attn_fwd_noalloc(const aa_attn_fwd_args* a, void* stream) {
 
 extern "C" int aa_attn_fwd(const aa_attn_fwd_args* a, void* stream) {
   clear_error();
+  if (a && a->hd == 384) {
+    if (a->dtype != AA_DTYPE_BF16) return fail(AA_EUNSUPPORTED, "only bf16 attention is implemented");
+    return attn_fwd_d384(a, device_cu_count(), (hipStream_t)stream);
+  }
   FwdParams p;
   if (int rc = prepare(a, p)) return rc;
   if (a->B == 0 || a->Sq == 0) return AA_OK;

@@ -123,6 +123,24 @@ __device__ __forceinline__ s16x4 ds_read_tr(const bf16* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(lds_void*)p);
 }
 
+// 32-bit LDS byte address of a pointer into __shared__ memory.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(lds_void*)p;
+}
+
+typedef __attribute__((address_space(3))) bf16x8 lds_bf16x8;
+
+// 16-byte read at an LDS byte address (ds_read_b128; constant parts of the
+// address fold into the instruction's offset field).
+__device__ __forceinline__ bf16x8 lds_ld16(uint32_t addr) {
+  return *(const lds_bf16x8*)(uintptr_t)addr;
+}
+
+// ds_read_b64_tr_b16 at an LDS byte address.
+__device__ __forceinline__ s16x4 lds_ld8_tr(uint32_t addr) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(uintptr_t)addr);
+}
+
 // Transposed operand (dt, c4) of a swizzled row tile; tr0 / tr1 are
 // swz_tr_rd(lane, 0 / 1).
 __device__ __forceinline__ bf16x8 read_tr_operand(const bf16* tile, int c4, int dt, int tr0,

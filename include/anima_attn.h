@@ -22,7 +22,8 @@
  *     aa_last_error() returns the calling thread's last message.
  *   - Only dtype AA_DTYPE_BF16 is implemented for activations; weights,
  *     rotary tables, LSE and padding logs are float32; key lengths int32.
- *   - hd (head_dim) must be 128.
+ *   - hd (head_dim) must be 128; aa_attn_fwd (and its workspace and no-alloc
+ *     forms) also takes 384, the VAE decoder's single-head attention.
  *
  * The reference (anima-flat) has no C FFI of its own: its path is Python
  * calling FlashAttention-4 (CuTe DSL) and Triton kernels. Each entry point
@@ -167,8 +168,9 @@ typedef struct aa_attn_fwd_args {
 } aa_attn_fwd_args;
 
 /* Bytes of device workspace aa_attn_fwd needs on the current device: fp32
- * partial results when the work items (256 queries of one (batch, head)) of
- * a partial last round of workgroups are split over key ranges, else 0. */
+ * partial results when the work items (256 queries of one (batch, head); 128
+ * at hd 384) of a partial last round of workgroups (at hd 384: of too few
+ * work items to fill the device) are split over key ranges, else 0. */
 size_t aa_attn_fwd_workspace(int64_t B, int64_t Sq, int64_t Sk, int64_t H, int64_t hd);
 
 /*
@@ -181,15 +183,18 @@ size_t aa_attn_fwd_workspace(int64_t B, int64_t Sq, int64_t Sk, int64_t H, int64
  *           src/attention.py:74-81 (anima_flat::fa_fwd_k), and with
  *           ln_pad != NULL also the ctx_scale pass of
  *           src/attention.py:156-180 (cross_attention_trimmed).
+ * With hd == 384 (one kernel for that width, plus a combine pass when its keys
+ * are split): replaces the VAE's mid-block attention, src/vae.py:239
+ * (ffpa_attn_func / SDPA on [B, 1, S, 384], vae.py:10-13, 230-241).
  */
 int aa_attn_fwd(const aa_attn_fwd_args* args, void* stream);
 
 /*
  * aa_attn_fwd without a caller workspace and without any allocation: the
- * split partials go to a fixed device array of 33,816,576 bytes that the
+ * split partials go to a fixed device array of 50,462,720 bytes that the
  * library holds on each device it runs on until the process ends (every
- * forward on a 256-CU device fits; a plan that needs more returns
- * AA_EUNSUPPORTED). args->workspace / workspace_bytes are ignored. Calls on
+ * forward, head_dim 128 or 384, on a 256-CU device fits; a plan that needs
+ * more returns AA_EUNSUPPORTED). args->workspace / workspace_bytes are ignored. Calls on
  * one device share that array: calls that overlap on one device (two streams
  * at once) race and must be serialised by the caller. Same results as
  * aa_attn_fwd (same kernels). No counterpart in the reference: for callers

@@ -38,21 +38,21 @@ def _args(L, q, k, v, out, lse, seqused, ln_pad):
     return a
 
 
-def _both(pkg, B, Sq, Sk, H, seed, lens=None):
+def _both(pkg, B, Sq, Sk, H, seed, lens=None, hd=128):
     """(out, lse) of aa_attn_fwd with a torch workspace and of aa_attn_fwd_noalloc."""
     L = pkg._lib
     lib = L.lib()
     g = torch.Generator().manual_seed(seed)
-    q, k, v = (ref.bf16_normal((B, S, H, 128), g).to(DEV, BF) for S in (Sq, Sk, Sk))
+    q, k, v = (ref.bf16_normal((B, S, H, hd), g).to(DEV, BF) for S in (Sq, Sk, Sk))
     seqused = ln_pad = None
     if lens is not None:
         seqused = torch.tensor(lens, dtype=torch.int32, device=DEV)
         ln_pad = torch.log(torch.tensor([float(Sk - n) for n in lens])).to(DEV)
     stream = torch.cuda.current_stream().cuda_stream
-    ws_bytes = lib.aa_attn_fwd_workspace(B, Sq, Sk, H, 128)
+    ws_bytes = lib.aa_attn_fwd_workspace(B, Sq, Sk, H, hd)
     results = []
     for noalloc in (False, True):
-        out = torch.full((B, Sq, H, 128), float("nan"), dtype=BF, device=DEV)
+        out = torch.full((B, Sq, H, hd), float("nan"), dtype=BF, device=DEV)
         lse = torch.full((B, H, Sq), float("nan"), dtype=torch.float32, device=DEV)
         a = _args(L, q, k, v, out, lse, seqused, ln_pad)
         if noalloc:
@@ -69,15 +69,17 @@ def _both(pkg, B, Sq, Sk, H, seed, lens=None):
 
 
 @pytest.mark.parametrize(
-    "B,Sq,Sk,H,lens,split",
+    "B,Sq,Sk,H,lens,split,hd",
     [
-        (1, 1024, 1024, 16, None, True),  # config 1: 64 work items, split 4 ways
-        (1, 300, 200, 3, [150], True),  # smaller, masked with the padding correction
-        (1, 4096, 4096, 16, None, False),  # config 2: one full round, no partials
+        (1, 1024, 1024, 16, None, True, 128),  # config 1: 64 work items, split 4 ways
+        (1, 300, 200, 3, [150], True, 128),  # smaller, masked with the padding correction
+        (1, 4096, 4096, 16, None, False, 128),  # config 2: one full round, no partials
+        (1, 16384, 16384, 1, None, True, 384),  # the VAE attention: 128 items x 2 key ranges
+        (1, 4096, 4096, 1, None, True, 384),  # smaller again: 32 items x 8 key ranges
     ],
 )
-def test_noalloc_matches_allocating_entry_point(pkg, B, Sq, Sk, H, lens, split):
-    ws_bytes, ((o1, l1), (o2, l2)), (q, k, v) = _both(pkg, B, Sq, Sk, H, seed=900 + Sq, lens=lens)
+def test_noalloc_matches_allocating_entry_point(pkg, B, Sq, Sk, H, lens, split, hd):
+    ws_bytes, ((o1, l1), (o2, l2)), (q, k, v) = _both(pkg, B, Sq, Sk, H, seed=900 + Sq, lens=lens, hd=hd)
     assert (ws_bytes > 0) == split
     assert torch.equal(o1, o2), f"out differs at {(o1 != o2).sum().item()} elements"
     assert torch.equal(l1, l2)
