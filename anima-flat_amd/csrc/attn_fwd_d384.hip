@@ -21,7 +21,9 @@
 //   is 16 scores per lane per tile, a third of the d=128 kernel's VALU work
 //   per MFMA, so a single wave can keep the matrix pipe busy if its VALU work
 //   runs between its MFMAs: each tile is two phases of 24 slots, each slot one
-//   MFMA plus a fixed slice of VALU work, pinned in place by sched_barrier:
+//   MFMA plus a fixed slice of VALU work, held in place by sched_barrier and
+//   by empty asm statements that anchor each slot's results (without them
+//   the compiler sinks the softmax into phase 2, next to its MFMA users):
 //     phase 1: S^T of tile t+1 (QK MFMAs) | P of tile t (fma, exp2, bf16,
 //              row sums)
 //     phase 2: O^T += V^T P^T of tile t   | row max of tile t+1
@@ -31,8 +33,9 @@
 // K/V staging: a 3-stage LDS ring of 48 KB stages (K and V of 32 keys as
 //   three 32-row x 128 sub-tiles each: K in the row-tile format, V in the
 //   swizzled one, tile_io.h), filled by DMA (global_load_lds_dwordx4). K of
-//   tile t+3 and V of tile t+2 are issued at the start of tile t, so each
-//   half has two tiles of lead time; waves 0-1 move K, waves 2-3 move V.
+//   tile t+3 and V of tile t+2 are issued during tile t's phase 1, one DMA
+//   instruction per MFMA slot, so each half has two tiles of lead time;
+//   waves 0-1 move K, waves 2-3 move V.
 #include <algorithm>
 #include <cmath>
 #include <string>
@@ -57,7 +60,7 @@ constexpr int kDmaPerTile = 12;            // DMA instructions per wave per K or
 constexpr int kMaxSplit = 8;
 constexpr float kRescaleThreshold = 8.0f;  // log2 units
 constexpr int kPf = 6;                     // operands read ahead of their MFMA
-constexpr int kQA = 12;                    // Q^T operands kept in AGPRs (the rest in VGPRs)
+constexpr int kQA = 16;                    // Q^T operands kept in AGPRs (the rest in VGPRs)
 
 struct Params {
   const bf16* q;
@@ -100,33 +103,30 @@ __device__ __forceinline__ void dma_row_quad(const bf16* base, int64_t rs, int n
   dma16_off<192>(src, dst + 1536);
 }
 
-// The MFMAs are inline asm with fixed register files: O^T accumulators in
-// AGPRs, S^T in VGPRs. Left to choose, the compiler puts every accumulator of
-// this kernel in one file and moves S^T or O^T across around each use, which
-// spills. It does not see these MFMAs' latency, so VALU code that reads their
-// results first runs a fence of wait states (fence_s, Wave::fence_o): an
-// MFMA result may be read no earlier than 18 wait states after issue.
+// Every MFMA is the compiler's builtin, so that the compiler pads the hazards
+// between an MFMA and the VALU code around it (a VALU write to an MFMA's
+// source registers right after its issue corrupts its operands; the
+// softmax work interleaved with the QK MFMAs sits exactly there). Register
+// files are steered instead: O^T stays in AGPRs because its zeros, rescales
+// and last reads are pinned there (Wave::setup, update_max, fence_o).
 __device__ __forceinline__ void mfma_o(f32x16& acc, bf16x8 a, bf16x8 b) {
-  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+  acc = mfma32(a, b, acc);
 }
-// S^T MFMA with the Q^T operand b in an AGPR (B_AGPR) or a VGPR.
-template <bool B_AGPR>
-__device__ __forceinline__ void mfma_s(f32x16& acc, bf16x8 a, bf16x8 b, bool first) {
-  if constexpr (B_AGPR) {
-    if (first)
-      asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(acc) : "v"(a), "a"(b));
-    else
-      asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(acc) : "v"(a), "a"(b));
-  } else {
-    if (first)
-      asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(acc) : "v"(a), "v"(b));
-    else
-      asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(acc) : "v"(a), "v"(b));
+
+// One tile's DMA work of one wave: three quads of 4 DMA instructions (16
+// rows x 4 chunks of 8 columns each), issued one instruction per MFMA slot of
+// phase 1. A wave with no tile left to move issues the same 12 instructions
+// into a dummy LDS area instead, so that every wave issues exactly 12 per
+// tile and one vmcnt(12) is the wait everywhere.
+struct DmaJob {
+  const bf16* src[3];  // this lane's global address of quad q (offsets 64 i bytes follow)
+  const bf16* dst[3];  // LDS destination of quad q (blocks at + 512 i elements)
+
+  template <int i>
+  __device__ __forceinline__ void issue() const {
+    dma16_off<64 * (i & 3)>(src[i >> 2], dst[i >> 2] + 512 * (i & 3));
   }
-}
-__device__ __forceinline__ void fence_s(f32x16& acc) {
-  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" : "+v"(acc));
-}
+};
 
 struct Item {
   int b, h, qblk, klen;
@@ -212,15 +212,15 @@ struct Wave {
       constexpr int i = decltype(I)::value;
       if constexpr (i >= kPf) {
         constexpr int op = i - kPf;
-        mfma_s<(op < kQA)>(acc, q[op % kPf], qreg[op], op == 0);
+        acc = mfma32(q[op % kPf], qreg[op], op == 0 ? f32x16{} : acc);
       }
       if constexpr (i < 24) q[i % kPf] = this->template k_op<i>(kb);
       __builtin_amdgcn_sched_barrier(0);
     });
-    fence_s(acc);
   }
 
-  // Orders VALU accesses of O after the last MFMA that wrote it.
+  // Keeps O in AGPRs up to this point and orders the VALU code that follows
+  // after every MFMA that wrote it.
   __device__ __forceinline__ void fence_o() {
     asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3"
                  : "+a"(o[0]), "+a"(o[1]), "+a"(o[2]), "+a"(o[3]), "+a"(o[4]), "+a"(o[5]),
@@ -249,7 +249,7 @@ struct Wave {
   // Phase 1: S^T of the next tile (kst, skipped when QK is false) with P of
   // the current tile s -> pb and the row sums in the same slots.
   template <bool QK>
-  __device__ __forceinline__ void phase1(const bf16* kst) {
+  __device__ __forceinline__ void phase1(const bf16* kst, const DmaJob& job) {
     const float mc = m_raw * c;
     const bf16x2 ones = {(bf16)1.0f, (bf16)1.0f};
     bf16x8 q[kPf];
@@ -259,9 +259,10 @@ struct Wave {
       constexpr int i = decltype(I)::value;
       if constexpr (QK && i >= kPf) {
         constexpr int op = i - kPf;
-        mfma_s<(op < kQA)>(sn, q[op % kPf], qreg[op], op == 0);
+        sn = mfma32(q[op % kPf], qreg[op], op == 0 ? f32x16{} : sn);
       }
       if constexpr (QK && i < 24) q[i % kPf] = this->template k_op<i>(kb);
+      if constexpr (QK && i >= 2 && i < 14) job.template issue<i - 2>();
       // P: one score per slot for slots 0-15, packed and summed in pairs.
       if constexpr (i < 16) {
         const float e = fast_exp2(fmaf(s[i], c, -mc));
@@ -272,11 +273,14 @@ struct Wave {
           pb[i >> 3][i & 7] = (bf16)e;
           const bf16x2 pair = {pb[i >> 3][(i & 7) - 1], pb[i >> 3][i & 7]};
           l[(i >> 1) & 1] = __builtin_amdgcn_fdot2_f32_bf16(pair, ones, l[(i >> 1) & 1], false);
+          // Anchored in this slot: left alone, the compiler sinks the whole
+          // P computation into phase 2, next to its MFMA users, where it
+          // stalls them instead of overlapping phase 1's.
+          asm volatile("" : "+v"(pb[i >> 3]), "+v"(l[(i >> 1) & 1]));
         }
       }
       __builtin_amdgcn_sched_barrier(0);
     });
-    if constexpr (QK) fence_s(sn);
   }
 
   // Phase 2: O^T += V^T P^T of the current tile (vst) with the row max of the
@@ -308,6 +312,7 @@ struct Wave {
         } else if constexpr (i == kPf + 6) {
           mt = pair_max(max3f(ma, mb, max2f(sn[14], sn[15])));
         }
+        asm volatile("" : "+v"(ma), "+v"(mb));
       }
       __builtin_amdgcn_sched_barrier(0);
     });
@@ -342,7 +347,9 @@ struct Wave {
 // and share its K/V tiles in that XCD's L2.
 __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void attn_fwd_d384_kernel(Params p) {
-  __shared__ __attribute__((aligned(1024))) bf16 lds[kStages * kStageElems];
+  // The ring, then 4 KB that DMAs with nothing to move write into.
+  __shared__ __attribute__((aligned(1024))) bf16 lds[kStages * kStageElems + 2048];
+  const bf16* dummy = lds + kStages * kStageElems;
 
   const int L = xcd_remap(blockIdx.x, gridDim.x);
   const int split = L / p.items;
@@ -364,29 +371,38 @@ void attn_fwd_d384_kernel(Params p) {
   const bf16* kp = p.k + it.b * p.ks0 + it.h * p.ks2;
   const bf16* vp = p.v + it.b * p.vs0 + it.h * p.vs2;
   auto stage = [&](int t) -> bf16* { return lds + (t % kStages) * kStageElems; };
-  // K of tile t (waves 0-1) / V of tile t (waves 2-3): 3 quads of 4 DMAs per wave.
-  auto issue_k = [&](int t) {
-    const int kb = (t0 + t) * kBN;
-    const int nrows = it.klen - kb;
-    const bf16* src = kp + (int64_t)kb * p.ks1;
-#pragma unroll
-    for (int qd = 0; qd < 3; ++qd) {
-      const int x = 3 * wave + qd;  // 0..5: chunk x / 2, row group x % 2
-      dma_row_quad(src + 128 * (x >> 1), p.ks1, nrows, stage(t) + (x >> 1) * kSub, x & 1, lane);
-    }
-  };
-  auto issue_v = [&](int t) {
-    const int kb = (t0 + t) * kBN;
-    const int nrows = it.klen - kb;
-    const bf16* src = vp + (int64_t)kb * p.vs1;
-#pragma unroll
-    for (int qd = 0; qd < 3; ++qd) {
-      const int x = 3 * (wave - 2) + qd;
-      dma_row_quad_swz(src + 128 * (x >> 1), p.vs1, nrows, stage(t) + (3 + (x >> 1)) * kSub,
-                       x & 1, lane);
-    }
-  };
   const bool k_mover = wave < 2;
+  // DMA job of tile t: K (waves 0-1, row tile) or V (waves 2-3, swizzled row
+  // tile), 3 quads per wave: quad x = 0..5 of the tensor covers chunk x / 2,
+  // row group x % 2. Rows past the tile's keys re-read its last key (their
+  // scores are masked). t >= n gives the dummy job.
+  auto job_of = [&](int t) -> DmaJob {
+    DmaJob j;
+    const int lq = lane >> 4;
+#pragma unroll
+    for (int qd = 0; qd < 3; ++qd) {
+      if (t >= n) {
+        j.src[qd] = kp + 8 * lq;
+        j.dst[qd] = dummy;
+        continue;
+      }
+      const int kb = (t0 + t) * kBN;
+      const int nrows = it.klen - kb;
+      const int x = 3 * (k_mover ? wave : wave - 2) + qd;
+      const int g = x & 1;
+      const int r = k_mover ? (lane & 15) : ((lane & 15) ^ (4 * lq));
+      const int row = min(16 * g + r, nrows - 1);
+      const bf16* base = k_mover ? kp + (int64_t)kb * p.ks1 : vp + (int64_t)kb * p.vs1;
+      const int64_t rs = k_mover ? p.ks1 : p.vs1;
+      j.src[qd] = base + (int64_t)row * rs + 128 * (x >> 1) + 8 * lq;
+      j.dst[qd] = stage(t) + ((k_mover ? 0 : kChunks) + (x >> 1)) * kSub + 4 * g * 512;
+    }
+    return j;
+  };
+  auto issue_now = [&](int t) {
+    const DmaJob j = job_of(t);
+    static_for<0, 12>([&](auto I) { j.template issue<decltype(I)::value>(); });
+  };
 
   // Q rows of this wave, three 128-wide chunks, staged in ring stages 1-2
   // (free until tile 1's DMA, issued after the barrier that follows every
@@ -396,10 +412,7 @@ void attn_fwd_d384_kernel(Params p) {
 #pragma unroll
   for (int j = 0; j < kChunks; ++j)
     stage_rows_in(qbase + 128 * j, p.qs1, qrow0, p.Sq, lane, qst + j * 4096);
-  if (n > 0) {
-    if (k_mover) issue_k(0);
-    else issue_v(0);
-  }
+  if (n > 0) issue_now(0);
   wait_dma();
   __syncthreads();
 #pragma unroll
@@ -412,47 +425,37 @@ void attn_fwd_d384_kernel(Params p) {
   __syncthreads();
 
   if (n > 0) {
-    // Lead: K of tiles 1, 2 and V of tile 1.
-    if (k_mover) {
-      if (n > 1) issue_k(1);
-      if (n > 2) issue_k(2);
-    } else if (n > 1) {
-      issue_v(1);
-    }
+    // Lead: K of tiles 1, 2 and V of tile 1 (or dummy jobs).
+    issue_now(1);
+    if (k_mover) issue_now(2);
     w.qk_plain(stage(0), w.s);
     const int kb0 = t0 * kBN;
     if (kb0 + kBN > it.klen) w.mask(w.s, kb0, it.klen);
     w.m_raw = w.row_max(w.s);
 
-    // Waits for K of tile t+1 and V of tile t, then publishes them; the DMAs
-    // issued one tile later (K of t+2 / V of t+1, 12 per wave) may still be
-    // in flight. K of t+3 then reuses the K half of tile t's stage (its QK ran
-    // in the last tile) and V of t+2 the V half of tile t-1's (its PV ran in
-    // the last tile).
-    auto next_tile = [&](int t) {
-      const bool later = k_mover ? (t + 2 < n) : (t + 1 < n);
-      if (later) asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
-      else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    // Tile t needs K of tile t+1 (QK) and V of tile t (PV). Every wave issues
+    // one job of 12 DMAs per tile, K movers three tiles ahead and V movers
+    // two, so at the top of tile t exactly one job (the last) may still be
+    // in flight; the barrier then publishes every wave's. The job issued in
+    // tile t, K of t+3 / V of t+2, reuses the K half of tile t's stage (its
+    // QK ran in tile t-1) / the V half of tile t-1's (its PV ran in tile t-1).
+    // The last tile runs the same body (one code path through the loop keeps
+    // the accumulators in place): its QK of a tile n reads stale LDS and is
+    // discarded, and neither the mask nor the max update runs for it.
+    for (int t = 0; t < n; ++t) {
+      asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
       __syncthreads();
-      if (k_mover) {
-        if (t + 3 < n) issue_k(t + 3);
-      } else if (t + 2 < n) {
-        issue_v(t + 2);
-      }
-    };
-    for (int t = 0; t < n - 1; ++t) {
-      next_tile(t);
-      w.phase1<true>(stage(t + 1));
+      const DmaJob job = job_of(k_mover ? t + 3 : t + 2);
+      w.phase1<true>(stage(t + 1), job);
+      const bool more = t + 1 < n;
       const int kbn = (t0 + t + 1) * kBN;
-      if (kbn + kBN > it.klen) w.mask(w.sn, kbn, it.klen);
+      if (more && kbn + kBN > it.klen) w.mask(w.sn, kbn, it.klen);
       w.phase2<true>(stage(t) + kChunks * kSub);
-      w.update_max();
+      if (more) w.update_max();
       w.s = w.sn;
     }
-    next_tile(n - 1);
-    w.phase1<false>(stage(n - 1));
-    w.phase2<false>(stage(n - 1) + kChunks * kSub);
   }
+  wait_dma();  // no DMA may land in LDS after the workgroup ends
 
   // Output: O / l (and the padding correction), or the range's partial.
   w.fence_o();
