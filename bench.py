@@ -17,7 +17,8 @@ profiles/attn_fwd_cfg2_pmc.txt.
 
 Extra fields report the other kernels of the path: prologue and head_norm
 HBM GB/s, masked cross-attention (config 3), forward+backward (config 5),
-and the 28-layer attention time of one CFG denoiser step at 1024x1024.
+the 28-layer attention time of one CFG denoiser step at 1024x1024, and the
+VAE decoder's head_dim-384 attention at 1024x1024.
 
 `cpu_baseline`: the reference's non-FA4 path, torch SDPA (math backend) in
 fp32 on the host CPU, on a bounded sample of config 2 (a subset of heads),
@@ -133,7 +134,7 @@ def copy_calibration(dev) -> None:
 
 
 PROFILE_CASES = ("self_cfg2", "self_cfg1", "prologue_cfg2", "head_norm_cfg3", "cross_cfg3",
-                 "cross_b2_512", "rowquant_cfg3", "prologue_bwd_cfg5")
+                 "cross_b2_512", "rowquant_cfg3", "prologue_bwd_cfg5", "vae_d384")
 
 
 def profile_case(name: str, steps: int, pkg, fp8, dev) -> dict:
@@ -174,6 +175,10 @@ def profile_case(name: str, steps: int, pkg, fp8, dev) -> dict:
         else:
             o_att = torch.randn(2, S, H * d, generator=g).to(dev, BF)
             fn = lambda: fp8.rowquant(o_att)
+    elif name == "vae_d384":
+        vae = importlib.import_module("anima_flat_amd.vae")
+        qv, kv_, vv = (torch.randn(1, 1, 16384, 384, generator=g).to(dev, BF) for _ in range(3))
+        fn = lambda: vae.attend(qv, kv_, vv)
     else:
         raise SystemExit(f"bench.py: unknown --profile-case {name!r} (one of {', '.join(PROFILE_CASES)})")
     with torch.no_grad():
@@ -529,6 +534,23 @@ def main() -> int:
                 "what": "as denoiser_step_attn_ms, cross-attn over the first seqused keys with the fused "
                         "padding correction (lengths from context_lengths, once per prompt)",
             }
+            # The VAE decoder's mid-block attention at 1024x1024 (src/vae.py:230-241): one head
+            # of 384 channels over 128 x 128 = 16384 latent positions.
+            vae = importlib.import_module("anima_flat_amd.vae")
+            Sv = 16384
+            qv, kv_, vv = (torch.randn(1, 1, Sv, 384, device=dev, dtype=BF) for _ in range(3))
+            with torch.no_grad():
+                vfn = lambda: vae.attend(qv, kv_, vv)
+                prewarm(vfn, 0.3)
+                _, us_v = time_launches(vfn, 10, 2)
+            fl_v = attn_flops(1, 1, Sv, Sv, 384)
+            extras["vae_attn_d384"] = {
+                "us": round(us_v * 1e3, 1),
+                "TFLOP/s": round(fl_v / (us_v * 1e-3) / 1e12, 1),
+                "pct_of_peak": round(100 * fl_v / (us_v * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 2),
+                "what": "vae.attend: B=1, 1 head, 16384 tokens, head_dim 384 (VAE mid-block at 1024x1024)",
+            }
+            del qv, kv_, vv
         result["extras"] = extras
         if "denoiser_step_attn_ms" in extras:
             result["per_step_attn_ms"] = extras["denoiser_step_attn_ms"]["ms"]
