@@ -205,53 +205,41 @@ __global__ __launch_bounds__(kBwdThreads) void norm_bwd_kernel(
   }
 }
 
-// First level of the weight-gradient reduction: block i sums chunks
-// kL1Chunks i .. kL1Chunks i + kL1Chunks - 1 of partial[nchunk][n] in order
-// into l1[i][n] (n <= 256, one thread per output, coalesced rows).
-constexpr int kL1Chunks = 16;
-__global__ __launch_bounds__(256) void reduce_partials_l1_kernel(const float* __restrict__ partial,
-                                                                 int64_t nchunk, int n,
-                                                                 float* __restrict__ l1) {
-  const int o = threadIdx.x;
-  if (o >= n) return;
-  const int64_t c0 = (int64_t)blockIdx.x * kL1Chunks;
-  float t[kL1Chunks];
-#pragma unroll
-  for (int i = 0; i < kL1Chunks; ++i) t[i] = c0 + i < nchunk ? partial[(c0 + i) * n + o] : 0.f;
-  float s = 0.f;
-#pragma unroll
-  for (int i = 0; i < kL1Chunks; ++i) s += t[i];
-  l1[(int64_t)blockIdx.x * n + o] = s;
-}
-
-// Sums partial[nchunk][n] over chunks in a fixed order: 4 interleaved lanes of
-// chunks per output (chunks p, p + 4, ...), combined in order. The loads of
-// kBatch consecutive terms are issued together and then added in sequence, so
-// the chain of adds does not wait on one load at a time. n <= 256.
-__global__ __launch_bounds__(1024) void reduce_partials_kernel(const float* __restrict__ partial,
-                                                               int64_t nchunk, int n,
-                                                               float* __restrict__ out0,
-                                                               float* __restrict__ out1) {
-  constexpr int kBatch = 16;
-  __shared__ float red[4][256];
-  const int o = threadIdx.x & 255;
-  const int p = threadIdx.x >> 8;
+// Weight-gradient reduction of partial[nchunk][n] (n <= 256 outputs) in one
+// launch, in a fixed order: block b owns outputs 8 b .. 8 b + 7; its 32 lane
+// groups r sum chunks r, r + 32, r + 64, ... in order (the loads of a batch
+// issued together, then added in sequence), and the 32 group sums are added
+// in order through LDS. (Folding this into norm_bwd_kernel's tail, the last
+// block of each group of chunks adding behind a device-scope atomic counter,
+// measured 105 us instead of ~30 for the whole backward: on the 8-XCD MI355X a
+// device-scope release fence writes back the XCD's L2, once per block.)
+constexpr int kRedOut = 8;     // outputs per block
+constexpr int kRedLanes = 32;  // lane groups per output
+__global__ __launch_bounds__(kRedOut * kRedLanes) void reduce_partials_kernel(
+    const float* __restrict__ partial, int64_t nchunk, int n, float* __restrict__ out0,
+    float* __restrict__ out1) {
+  constexpr int kBatch = 8;
+  __shared__ float red[kRedLanes][kRedOut];
+  const int oo = threadIdx.x % kRedOut;
+  const int r = threadIdx.x / kRedOut;
+  const int o = blockIdx.x * kRedOut + oo;
   float s = 0.f;
   if (o < n) {
-    int64_t c = p;
-    for (; c + 4 * (kBatch - 1) < nchunk; c += 4 * kBatch) {
+    int64_t c = r;
+    for (; c + (int64_t)kRedLanes * (kBatch - 1) < nchunk; c += (int64_t)kRedLanes * kBatch) {
       float t[kBatch];
 #pragma unroll
-      for (int i = 0; i < kBatch; ++i) t[i] = partial[(c + 4 * i) * n + o];
+      for (int i = 0; i < kBatch; ++i) t[i] = partial[(c + (int64_t)kRedLanes * i) * n + o];
 #pragma unroll
       for (int i = 0; i < kBatch; ++i) s += t[i];
     }
-    for (; c < nchunk; c += 4) s += partial[c * n + o];
+    for (; c < nchunk; c += kRedLanes) s += partial[c * n + o];
   }
-  red[p][o] = s;
+  red[r][oo] = s;
   __syncthreads();
-  if (p == 0 && o < n) {
-    const float t = ((red[0][o] + red[1][o]) + red[2][o]) + red[3][o];
+  if (r == 0 && o < n) {
+    float t = 0.f;
+    for (int rr = 0; rr < kRedLanes; ++rr) t += red[rr][oo];
     if (o < kHd) out0[o] = t;
     else out1[o - kHd] = t;
   }
@@ -268,22 +256,17 @@ __global__ void zero_f32_kernel(float* __restrict__ a, float* __restrict__ b, in
 constexpr int kBwdRows = 8;  // tokens per block: enough blocks to keep the CUs' loads in flight
 
 static int64_t bwd_chunks(int64_t B, int64_t S) { return (B * S + kBwdRows - 1) / kBwdRows; }
-static int64_t l1_blocks(int64_t nchunk) { return (nchunk + kL1Chunks - 1) / kL1Chunks; }
-
-// Weight-gradient workspace: the per-chunk partials, then the first-level sums.
+// Weight-gradient workspace: the per-chunk partials.
 static size_t wgrad_workspace(int64_t B, int64_t S, int64_t n) {
-  const int64_t nchunk = bwd_chunks(B, S);
-  return (size_t)(nchunk + l1_blocks(nchunk)) * (size_t)n * sizeof(float);
+  return (size_t)bwd_chunks(B, S) * (size_t)n * sizeof(float);
 }
 
-// Two-level fixed-order sum of partial[nchunk][n] into out0 / out1 (outputs
-// 0..127 / 128..255).
+// Fixed-order sum of partial[nchunk][n] into out0 / out1 (outputs 0..127 /
+// 128..255).
 static void reduce_wgrad(float* partial, int64_t nchunk, int n, float* out0, float* out1,
                          hipStream_t st) {
-  float* l1 = partial + nchunk * n;
-  const int64_t nl1 = l1_blocks(nchunk);
-  reduce_partials_l1_kernel<<<dim3((unsigned)nl1), 256, 0, st>>>(partial, nchunk, n, l1);
-  reduce_partials_kernel<<<1, 1024, 0, st>>>(l1, nl1, n, out0, out1);
+  reduce_partials_kernel<<<dim3((unsigned)((n + kRedOut - 1) / kRedOut)), kRedOut * kRedLanes, 0,
+                           st>>>(partial, nchunk, n, out0, out1);
 }
 
 static int check_common(int64_t B, int64_t S, int64_t H, int64_t hd, int dtype) {

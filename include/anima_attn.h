@@ -109,7 +109,7 @@ int aa_head_norm_fwd(const void* x, void* y, const float* weight,
                      float eps, int dtype, void* stream);
 
 /* Bytes of workspace aa_qkv_norm_rope_bwd needs (weight-grad partials: one
- * 2*hd float record per 8 tokens, then one per 16 such records). */
+ * 2*hd float record per 8 tokens). */
 size_t aa_qkv_norm_rope_bwd_workspace(int64_t B, int64_t S, int64_t H, int64_t hd);
 
 /*

@@ -90,8 +90,9 @@ def test_workspace_sizes(lib):
     assert lib.aa_attn_bwd_workspace(1, 0, 77, 3, 128) == 0
     # weight-gradient partials: one [2][128] (or [128]) fp32 record per 8 tokens,
     # then one per 16 records (the two-level reduction).
-    assert lib.aa_qkv_norm_rope_bwd_workspace(1, 4096, 16, 128) == (512 + 32) * 2 * 128 * 4
-    assert lib.aa_head_norm_bwd_workspace(2, 9, 5, 128) == (3 + 1) * 128 * 4
+    # One record of weight-gradient partial sums per 8 tokens.
+    assert lib.aa_qkv_norm_rope_bwd_workspace(1, 4096, 16, 128) == 512 * 2 * 128 * 4
+    assert lib.aa_head_norm_bwd_workspace(2, 9, 5, 128) == 3 * 128 * 4
     # one int32 per 32 context rows per item
     assert lib.aa_context_lengths_workspace(3, 77) == 3 * 3 * 4
     assert lib.aa_context_lengths_workspace(0, 77) == 0

@@ -70,6 +70,41 @@ def test_qkv_norm_rope_backward(pkg, dev, B, S, H):
     parity(kw.grad, edkw, max_abs=2e-2 * max(1.0, edkw.abs().max().item()), name="dk_weight")
 
 
+@pytest.mark.parametrize("B,S,H", [(1, 4096, 16), (1, 1000, 4), (2, 50, 3)])
+def test_qkv_norm_rope_backward_deterministic_c_abi(pkg, dev, B, S, H):
+    """Two calls through the C ABI on one (uninitialised) workspace give the
+    op's results bit for bit: the weight-gradient reduction sums in a fixed
+    order whatever the partials' layout of blocks (512, 125 and 13 chunks of 8
+    tokens)."""
+    import ctypes
+
+    L = pkg._lib
+    lib = L.lib()
+    eps = 1e-6
+    inp = _inputs(B, S, H, seed=300 + S)
+    g = torch.Generator().manual_seed(301)
+    qkv = inp["qkv"].to(dev, BF)
+    dq, dk, dv = (ref.bf16_normal((B, S, H, 128), g).to(dev, BF) for _ in range(3))
+    qw, kw = inp["q_weight"].to(dev), inp["k_weight"].to(dev)
+    cos, sin = inp["cos"].to(dev), inp["sin"].to(dev)
+    expected = torch.ops.anima_flat.qkv_norm_rope_bwd(qkv, dq, dk, dv, qw, kw, cos, sin, H, eps)
+    ws_bytes = lib.aa_qkv_norm_rope_bwd_workspace(B, S, H, 128)
+    ws = torch.full((ws_bytes // 4,), float("nan"), dtype=torch.float32, device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+    for call in range(2):
+        dqkv = torch.full_like(qkv, float("nan"))
+        dqw = torch.full((128,), float("nan"), device=dev)
+        dkw = torch.full((128,), float("nan"), device=dev)
+        rc = lib.aa_qkv_norm_rope_bwd(
+            qkv.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), dqkv.data_ptr(),
+            qw.data_ptr(), kw.data_ptr(), cos.data_ptr(), sin.data_ptr(), dqw.data_ptr(),
+            dkw.data_ptr(), ws.data_ptr(), ws_bytes, B, S, H, 128, ctypes.c_float(eps), 0, stream)
+        L.check(rc, "qkv_norm_rope_bwd")
+        torch.cuda.synchronize()
+        assert torch.equal(dqkv, expected[0]), f"call {call}: dqkv"
+        assert torch.equal(dqw, expected[1]) and torch.equal(dkw, expected[2]), f"call {call}: weight grads"
+
+
 @pytest.mark.parametrize("B,S,H", [(2, 4096, 16), (1, 9, 5)])
 def test_head_norm_forward_backward(pkg, dev, B, S, H):
     eps = 1e-6
