@@ -41,6 +41,12 @@ __device__ __forceinline__ float round_bf16(float x) {
 // 16-byte global load/store helpers (the pointer must be 16-byte aligned).
 __device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 __device__ __forceinline__ void st16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
+// Streaming store of an output no kernel of this launch reads back: the
+// nontemporal hint keeps it from allocating in L2, which measured 4-25% faster
+// on the HBM-bound kernels (prologue 11.9 -> 10.4 us, rowquant 9.9 -> 7.6 us).
+__device__ __forceinline__ void st16_nt(void* p, u32x4 v) {
+  __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
+}
 __device__ __forceinline__ f32x4 ldf4(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
 
 // Unpack 8 bf16 (one 16-byte chunk) into floats.

@@ -24,8 +24,8 @@ __device__ __forceinline__ void norm_section(const bf16* src, bf16* dst, const f
   load_section(src, j, x);
   float oa[8], ob[8];
   norm_rotate<ROTATE>(x, w, cos, sin, pos, j, eps, oa, ob);
-  st16(dst + 8 * j, pack8(oa));
-  st16(dst + kHalf + 8 * j, pack8(ob));
+  st16_nt(dst + 8 * j, pack8(oa));
+  st16_nt(dst + kHalf + 8 * j, pack8(ob));
 }
 
 // qkv [ntok, 3*H*128] -> q, k [ntok, H, 128] (+ v copy). Sections of a token:
@@ -49,8 +49,8 @@ __global__ __launch_bounds__(256) void qkv_norm_rope_fwd_kernel(
   const bf16* src = qkv + token * 3 * width + which * width + head * kHd;
   const int64_t dst_off = token * width + head * kHd;
   if (WITH_V && which == 2) {
-    st16(v + dst_off + 8 * j, ld16(src + 8 * j));
-    st16(v + dst_off + kHalf + 8 * j, ld16(src + kHalf + 8 * j));
+    st16_nt(v + dst_off + 8 * j, ld16(src + 8 * j));
+    st16_nt(v + dst_off + kHalf + 8 * j, ld16(src + kHalf + 8 * j));
     return;
   }
   const int64_t pos = token % S;
@@ -119,8 +119,8 @@ __device__ __forceinline__ void norm_section_bwd(const bf16* src, const bf16* dy
     ga[i] += d.a[i] * xa[i];
     gb[i] += d.b[i] * xb[i];
   }
-  st16(dx + 8 * j, pack8(oa));
-  st16(dx + kHalf + 8 * j, pack8(ob));
+  st16_nt(dx + 8 * j, pack8(oa));
+  st16_nt(dx + kHalf + 8 * j, pack8(ob));
 }
 
 constexpr int kBwdThreads = 256;
@@ -184,7 +184,7 @@ __global__ __launch_bounds__(kBwdThreads) void norm_bwd_kernel(
     for (int rr = 0; rr < nrows; ++rr) {
       const int64_t token = first + rr;
       for (int c = tid; c < (int)(width / 8); c += kBwdThreads) {
-        st16(dx + token * xrow + 2 * width + 8 * c, ld16(dv + token * width + 8 * c));
+        st16_nt(dx + token * xrow + 2 * width + 8 * c, ld16(dv + token * width + 8 * c));
       }
     }
   }

@@ -205,7 +205,7 @@ __device__ __forceinline__ void stage_rows_out(bf16* base, int64_t rs, int row0,
   for (int i = 0; i < 8; ++i) {
     const int r = (lane >> 4) + 4 * i;
     const u32x4 v = *reinterpret_cast<const u32x4*>(stage + stage_at(r, c));
-    if (row0 + r < nrows) st16(base + (int64_t)(row0 + r) * rs + 8 * c, v);
+    if (row0 + r < nrows) st16_nt(base + (int64_t)(row0 + r) * rs + 8 * c, v);
   }
 }
 
