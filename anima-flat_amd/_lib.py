@@ -36,6 +36,15 @@ _PROTOTYPES: dict[str, tuple[object, list[object]]] = {
         c_int,
         [c_void_p] * 4 + [c_void_p] * 4 + [_I64] * 4 + [c_float, c_int, c_void_p],
     ),
+    "aa_proj_head_norm": (
+        c_int,
+        [c_void_p, _I64, c_void_p, _I64, c_void_p, c_void_p] + [_I64] * 4 + [c_float, c_int, c_void_p],
+    ),
+    "aa_kv_proj_norm": (
+        c_int,
+        [c_void_p, _I64, c_void_p, _I64, c_void_p, c_void_p, c_void_p] + [_I64] * 4
+        + [c_float, c_int, c_void_p],
+    ),
     "aa_qkv_proj_norm_rope": (
         c_int,
         [c_void_p, _I64, c_void_p] + [c_void_p] * 3 + [c_void_p] * 4 + [_I64] * 4

@@ -27,6 +27,8 @@
 // within the range in groups of 4 token tiles x all column tiles, so the 32
 // workgroups an XCD runs at once share 4 X tiles and 8 W tiles in its L2.
 // With an odd number of sections (3 H) the last column tile holds one.
+#include <string>
+
 #include "aa_common.h"
 #include "norm_rope.h"
 #include "tile_io.h"
@@ -42,15 +44,20 @@ constexpr int kPXElems = kPM * kPK;                 // 16 KiB
 constexpr int kPStageElems = kPXElems + kPN * kPK;  // + 16 KiB of W
 constexpr int kPGroupM = 4;                         // token tiles per work-order group
 
+// The projection's output columns are nseg segments of H sections of 128:
+// segment g goes to out[g] ([ntok, H, 128]), RMS-normalised with weight nw[g]
+// (then rotated when rope[g]) or copied when nw[g] is null.
+//   qkv + prologue (model.py:308-316): q (norm, rope), k (norm, rope), v (copy)
+//   xq + head_norm (model.py:324):     q (norm)
+//   xkv + k-norm (model.py:256-258):   k (norm), v (copy)
 struct ProjParams {
-  const bf16* x;  // hidden states, row r at x + r * xs
+  const bf16* x;  // input rows, row r at x + r * xs
   int64_t xs;
-  const bf16* w;  // [3 H 128, K]
-  bf16* q;        // [ntok, H, 128] each
-  bf16* k;
-  bf16* v;
-  const float* qw;
-  const float* kw;
+  const bf16* w;  // [nseg H 128, K]
+  bf16* out[3];
+  const float* nw[3];
+  int rope[3];
+  int nseg;
   const float* cos;
   const float* sin;
   int64_t ntok;
@@ -78,7 +85,7 @@ __global__ __launch_bounds__(kPThreads) void qkv_proj_kernel(ProjParams p) {
   const int wave = tid >> 6;
 
   // Tile of this workgroup: token tile mt, sections 2 nt and 2 nt + 1.
-  const int nsec = 3 * p.H;
+  const int nsec = p.nseg * p.H;
   const int ntn = (nsec + 1) / 2;
   const int total = p.mtiles * ntn;
   const int L = xcd_remap(blockIdx.x, total);
@@ -185,8 +192,9 @@ __global__ __launch_bounds__(kPThreads) void qkv_proj_kernel(ProjParams p) {
     const int gsec = 2 * nt + sc;
     const int seg = gsec / p.H;
     const int head = gsec - seg * p.H;
-    bf16* out = seg == 0 ? p.q : (seg == 1 ? p.k : p.v);
-    const float* nw = seg == 0 ? p.qw : p.kw;
+    bf16* out = p.out[seg];
+    const float* nw = p.nw[seg];
+    const bool rope = p.rope[seg] != 0;
     const bf16* tile = lds + sc * (kPM * kHd);
     for (int r = grp; r < nrows; r += kPThreads / 8) {
       const u32x4 ra = *reinterpret_cast<const u32x4*>(tile + r * 128 + ((j ^ (r & 15)) * 8));
@@ -194,17 +202,18 @@ __global__ __launch_bounds__(kPThreads) void qkv_proj_kernel(ProjParams p) {
           *reinterpret_cast<const u32x4*>(tile + r * 128 + (((8 + j) ^ (r & 15)) * 8));
       const int64_t token = row0 + r;
       bf16* dst = out + (token * p.H + head) * kHd;
-      if (seg == 2) {
-        st16(dst + 8 * j, ra);
-        st16(dst + kHalf + 8 * j, rb);
+      if (!nw) {
+        st16_nt(dst + 8 * j, ra);
+        st16_nt(dst + kHalf + 8 * j, rb);
       } else {
         Section x;
         unpack8(ra, x.a);
         unpack8(rb, x.b);
         float oa[8], ob[8];
-        norm_rotate<true>(x, nw, p.cos, p.sin, token % p.S, j, p.eps, oa, ob);
-        st16(dst + 8 * j, pack8(oa));
-        st16(dst + kHalf + 8 * j, pack8(ob));
+        if (rope) norm_rotate<true>(x, nw, p.cos, p.sin, token % p.S, j, p.eps, oa, ob);
+        else norm_rotate<false>(x, nw, nullptr, nullptr, 0, j, p.eps, oa, ob);
+        st16_nt(dst + 8 * j, pack8(oa));
+        st16_nt(dst + kHalf + 8 * j, pack8(ob));
       }
     }
   }
@@ -214,37 +223,50 @@ __global__ __launch_bounds__(kPThreads) void qkv_proj_kernel(ProjParams p) {
 
 using namespace aa;
 
-extern "C" int aa_qkv_proj_norm_rope(const void* hid, int64_t hid_row_stride, const void* weight,
-                                     void* q, void* k, void* v, const float* q_weight,
-                                     const float* k_weight, const float* cos, const float* sin,
-                                     int64_t B, int64_t S, int64_t H, int64_t hd, float eps,
-                                     int dtype, void* stream) {
-  clear_error();
-  if (dtype != AA_DTYPE_BF16) return fail(AA_EUNSUPPORTED, "only bf16 activations are implemented");
+// Validates and launches one fused projection (nseg segments of H sections).
+// What the epilogue does with one output segment.
+enum SegMode { kCopy = 0, kNorm = 1, kNormRope = 2 };
+
+static int launch_proj(const char* what, const void* hid, int64_t hid_row_stride, const void* weight,
+                       int64_t K, int nseg, void* const* outs, const float* const* nws,
+                       const int* modes, const float* cos, const float* sin, int64_t B, int64_t S,
+                       int64_t H, int64_t hd, float eps, int dtype, hipStream_t st) {
+  const std::string w = what;
   if (hd != kHd) return fail(AA_EUNSUPPORTED, "head_dim must be 128");
-  if (B < 0 || S < 0 || H <= 0 || H > 64) return fail(AA_EINVAL, "qkv_proj: bad B/S/H (H <= 64)");
-  const int64_t K = H * kHd;
+  if (dtype != AA_DTYPE_BF16) return fail(AA_EUNSUPPORTED, "only bf16 activations are implemented");
+  if (B < 0 || S < 0 || H <= 0 || H > 64) return fail(AA_EINVAL, w + ": bad B/S/H (H <= 64)");
+  if (K <= 0 || K % kPK != 0 || K > (1 << 20))
+    return fail(AA_EUNSUPPORTED, w + ": the input width must be a positive multiple of 32");
   if (B * S == 0) return AA_OK;
-  if (!hid || !weight || !q || !k || !v || !q_weight || !k_weight || !cos || !sin)
-    return fail(AA_EINVAL, "qkv_proj: null pointer");
+  if (!hid || !weight) return fail(AA_EINVAL, w + ": null pointer");
+  bool any_rope = false;
+  for (int g = 0; g < nseg; ++g) {
+    if (!outs[g] || (modes[g] != kCopy && !nws[g])) return fail(AA_EINVAL, w + ": null pointer");
+    if (!aligned16(outs[g]) || (modes[g] != kCopy && !aligned16(nws[g])))
+      return fail(AA_EINVAL, w + ": pointers must be 16-byte aligned");
+    any_rope = any_rope || modes[g] == kNormRope;
+  }
+  if (any_rope && (!cos || !sin)) return fail(AA_EINVAL, w + ": null pointer");
+  if (any_rope && (!aligned16(cos) || !aligned16(sin)))
+    return fail(AA_EINVAL, w + ": pointers must be 16-byte aligned");
   if (hid_row_stride < K || hid_row_stride % 8 != 0)
-    return fail(AA_EINVAL, "qkv_proj: hidden row stride must be >= H*128 and a multiple of 8");
-  if (!aligned16(hid) || !aligned16(weight) || !aligned16(q) || !aligned16(k) || !aligned16(v) ||
-      !aligned16(q_weight) || !aligned16(k_weight) || !aligned16(cos) || !aligned16(sin))
-    return fail(AA_EINVAL, "qkv_proj: pointers must be 16-byte aligned");
+    return fail(AA_EINVAL, w + ": input row stride must be >= the input width and a multiple of 8");
+  if (!aligned16(hid) || !aligned16(weight))
+    return fail(AA_EINVAL, w + ": pointers must be 16-byte aligned");
   const int64_t ntok = B * S;
   const int64_t mtiles = (ntok + kPM - 1) / kPM;
-  const int64_t total = mtiles * ((3 * H + 1) / 2);
-  if (total > 0x7fffffff) return fail(AA_EUNSUPPORTED, "qkv_proj: too many tokens");
+  const int64_t total = mtiles * ((nseg * H + 1) / 2);
+  if (total > 0x7fffffff) return fail(AA_EUNSUPPORTED, w + ": too many tokens");
   ProjParams p;
   p.x = (const bf16*)hid;
   p.xs = hid_row_stride;
   p.w = (const bf16*)weight;
-  p.q = (bf16*)q;
-  p.k = (bf16*)k;
-  p.v = (bf16*)v;
-  p.qw = q_weight;
-  p.kw = k_weight;
+  for (int g = 0; g < 3; ++g) {
+    p.out[g] = g < nseg ? (bf16*)outs[g] : nullptr;
+    p.nw[g] = g < nseg && modes[g] != kCopy ? nws[g] : nullptr;
+    p.rope[g] = g < nseg && modes[g] == kNormRope;
+  }
+  p.nseg = nseg;
   p.cos = cos;
   p.sin = sin;
   p.ntok = ntok;
@@ -253,6 +275,43 @@ extern "C" int aa_qkv_proj_norm_rope(const void* hid, int64_t hid_row_stride, co
   p.K = (int)K;
   p.mtiles = (int)mtiles;
   p.eps = eps;
-  qkv_proj_kernel<<<dim3((unsigned)total), kPThreads, 0, (hipStream_t)stream>>>(p);
-  return check_launch("qkv_proj_norm_rope");
+  qkv_proj_kernel<<<dim3((unsigned)total), kPThreads, 0, st>>>(p);
+  return check_launch(what);
+}
+
+extern "C" int aa_qkv_proj_norm_rope(const void* hid, int64_t hid_row_stride, const void* weight,
+                                     void* q, void* k, void* v, const float* q_weight,
+                                     const float* k_weight, const float* cos, const float* sin,
+                                     int64_t B, int64_t S, int64_t H, int64_t hd, float eps,
+                                     int dtype, void* stream) {
+  clear_error();
+  void* outs[3] = {q, k, v};
+  const float* nws[3] = {q_weight, k_weight, nullptr};
+  const int modes[3] = {kNormRope, kNormRope, kCopy};
+  return launch_proj("qkv_proj", hid, hid_row_stride, weight, H * hd, 3, outs, nws, modes, cos,
+                     sin, B, S, H, hd, eps, dtype, (hipStream_t)stream);
+}
+
+extern "C" int aa_proj_head_norm(const void* x, int64_t x_row_stride, const void* weight,
+                                 int64_t K, void* y, const float* norm_weight, int64_t B,
+                                 int64_t S, int64_t H, int64_t hd, float eps, int dtype,
+                                 void* stream) {
+  clear_error();
+  void* outs[1] = {y};
+  const float* nws[1] = {norm_weight};
+  const int modes[1] = {kNorm};
+  return launch_proj("proj_head_norm", x, x_row_stride, weight, K, 1, outs, nws, modes, nullptr,
+                     nullptr, B, S, H, hd, eps, dtype, (hipStream_t)stream);
+}
+
+extern "C" int aa_kv_proj_norm(const void* ctx, int64_t ctx_row_stride, const void* weight,
+                               int64_t K, void* k, void* v, const float* k_weight, int64_t B,
+                               int64_t S, int64_t H, int64_t hd, float eps, int dtype,
+                               void* stream) {
+  clear_error();
+  void* outs[2] = {k, v};
+  const float* nws[2] = {k_weight, nullptr};
+  const int modes[2] = {kNorm, kCopy};
+  return launch_proj("kv_proj_norm", ctx, ctx_row_stride, weight, K, 2, outs, nws, modes, nullptr,
+                     nullptr, B, S, H, hd, eps, dtype, (hipStream_t)stream);
 }

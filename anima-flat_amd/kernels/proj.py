@@ -1,13 +1,14 @@
 """Fused input projections of the attention block (inference), opt-in.
 
 Not part of the reference's API and not imported by the package: import
-`anima_flat_amd.kernels.proj` to use it. Its op lives in the `anima_flat_amd::`
-namespace so it cannot collide with an `anima_flat::` op.
+`anima_flat_amd.kernels.proj` to use it. Its ops live in the `anima_flat_amd::`
+namespace so they cannot collide with an `anima_flat::` op.
 
-`qkv_proj_norm_rope` = the block's `b.qkv(hid)` projection followed by
-`qkv_norm_rope` (src/model.py:308-316) as one kernel (aa_qkv_proj_norm_rope):
-the [B, S, 3 * D] projection output stays on chip, q and k are RMS-normalised
-and rotated in the GEMM's epilogue, v is written as projected.
+One GEMM kernel (csrc/qkv_proj.hip) with the normalisation in its epilogue, so
+the projection output never reaches memory:
+  qkv_proj_norm_rope  the block's `b.qkv(hid)` + `qkv_norm_rope` (src/model.py:308-316)
+  proj_head_norm      `b.xq(hid)` + `head_norm` (src/model.py:324)
+  kv_proj_norm        `b.xkv(ctx)` + the key-side RMSNorm (src/model.py:256-258)
 """
 
 from __future__ import annotations
@@ -96,3 +97,117 @@ def qkv_proj_norm_rope(hid, weight, q_weight, k_weight, cos, sin, heads, eps=1e-
     return _qkv_proj_norm_rope(
         hid, weight, q_weight.contiguous(), k_weight.contiguous(), cos.contiguous(), sin.contiguous(), heads, eps
     )
+
+
+def _rows_ok(x: torch.Tensor) -> bool:
+    """[B, S, K] with unit last-dim stride and uniform rows (one row stride)."""
+    return x.ndim == 3 and x.stride(-1) == 1 and x.stride(0) == x.shape[1] * x.stride(1)
+
+
+@custom_op("anima_flat_amd::proj_head_norm", mutates_args=())
+def _proj_head_norm(
+    x: torch.Tensor, weight: torch.Tensor, norm_weight: torch.Tensor, heads: int, eps: float
+) -> torch.Tensor:
+    B, S, K = x.shape
+    hd = norm_weight.numel()
+    y = x.new_empty((B, S, heads, hd))
+    with torch.cuda.device(x.device):
+        _lib.check(
+            _lib.lib().aa_proj_head_norm(
+                x.data_ptr(), x.stride(1), weight.data_ptr(), K, y.data_ptr(),
+                _f32(norm_weight).data_ptr(), B, S, heads, hd, eps, _lib.dtype_code(x),
+                _lib.stream(x),
+            ),
+            "proj_head_norm",
+        )
+    return y
+
+
+@_proj_head_norm.register_fake
+def _(x, weight, norm_weight, heads, eps):
+    B, S, _ = x.shape
+    return x.new_empty((B, S, heads, norm_weight.numel()))
+
+
+def proj_head_norm(x, weight, norm_weight, heads, eps=1e-5):
+    """`head_norm(F.linear(x, weight), norm_weight, heads, eps)` as one kernel: the
+    cross-attention query projection and its per-head RMSNorm
+    (`head_norm(b.xq(hid), b.xq_norm, c.heads, c.qk_eps)`, src/model.py:324), with
+    the projection output kept on chip. Inference only (no autograd).
+
+    Args:
+        x: `[B, S, K]` bf16 (K a multiple of 32); rows may be strided (last-dim stride 1).
+        weight: `[heads * head_dim, K]` bf16, contiguous (nn.Linear, no bias).
+        norm_weight: RMSNorm weight `[head_dim]`.
+        heads, eps: as for `head_norm`.
+
+    Returns:
+        `[B, S, heads, head_dim]`, contiguous.
+    """
+    _check(x, weight, norm_weight)
+    hd = norm_weight.numel()
+    _check_hd(hd)
+    if not _rows_ok(x):
+        raise ValueError("x must be [B, S, K] with unit last-dim stride and uniform rows")
+    if not weight.is_contiguous() or tuple(weight.shape) != (heads * hd, x.shape[-1]) or weight.dtype != x.dtype:
+        raise ValueError("weight must be a contiguous [heads * head_dim, K] matrix of x's dtype")
+    if torch.is_grad_enabled() and (x.requires_grad or weight.requires_grad or norm_weight.requires_grad):
+        raise RuntimeError("proj_head_norm has no backward: use F.linear + head_norm for training")
+    return _proj_head_norm(x, weight, norm_weight.contiguous(), heads, eps)
+
+
+@custom_op("anima_flat_amd::kv_proj_norm", mutates_args=())
+def _kv_proj_norm(
+    ctx: torch.Tensor, weight: torch.Tensor, k_weight: torch.Tensor, heads: int, eps: float
+) -> tuple[torch.Tensor, torch.Tensor]:
+    B, S, K = ctx.shape
+    hd = k_weight.numel()
+    k = ctx.new_empty((B, S, heads, hd))
+    v = torch.empty_like(k)
+    with torch.cuda.device(ctx.device):
+        _lib.check(
+            _lib.lib().aa_kv_proj_norm(
+                ctx.data_ptr(), ctx.stride(1), weight.data_ptr(), K, k.data_ptr(), v.data_ptr(),
+                _f32(k_weight).data_ptr(), B, S, heads, hd, eps, _lib.dtype_code(ctx),
+                _lib.stream(ctx),
+            ),
+            "kv_proj_norm",
+        )
+    return k, v
+
+
+@_kv_proj_norm.register_fake
+def _(ctx, weight, k_weight, heads, eps):
+    B, S, _ = ctx.shape
+    k = ctx.new_empty((B, S, heads, k_weight.numel()))
+    return k, torch.empty_like(k)
+
+
+def kv_proj_norm(ctx, weight, k_weight, heads, eps=1e-5):
+    """One layer's context keys and values with the key-side RMSNorm fused
+    (src/model.py:256-258, in encode_context):
+    `k, v = b.xkv(ctx).view(B, S, 2, heads, hd).unbind(2)` then
+    `k = F.rms_norm(k, (hd,), b.xk_norm.to(k.dtype), eps)`, as one kernel with the
+    projection output kept on chip. Inference only (no autograd).
+
+    Args:
+        ctx: `[B, S, K]` bf16 text context (K = text_dim, a multiple of 32); rows may
+            be strided (last-dim stride 1).
+        weight: `[2 * heads * head_dim, K]` bf16, contiguous (nn.Linear, no bias).
+        k_weight: RMSNorm weight `[head_dim]`; applied in the activation dtype as
+            F.rms_norm does, so pass `b.xk_norm.to(ctx.dtype)` as the reference does.
+        heads, eps: as for `head_norm`.
+
+    Returns:
+        `(k, v)`, each a contiguous `[B, S, heads, head_dim]`.
+    """
+    _check(ctx, weight, k_weight)
+    hd = k_weight.numel()
+    _check_hd(hd)
+    if not _rows_ok(ctx):
+        raise ValueError("ctx must be [B, S, K] with unit last-dim stride and uniform rows")
+    if not weight.is_contiguous() or tuple(weight.shape) != (2 * heads * hd, ctx.shape[-1]) or weight.dtype != ctx.dtype:
+        raise ValueError("weight must be a contiguous [2 * heads * head_dim, K] matrix of ctx's dtype")
+    if torch.is_grad_enabled() and (ctx.requires_grad or weight.requires_grad or k_weight.requires_grad):
+        raise RuntimeError("kv_proj_norm has no backward: use F.linear + F.rms_norm for training")
+    return _kv_proj_norm(ctx, weight, k_weight.contiguous(), heads, eps)

@@ -134,7 +134,8 @@ def copy_calibration(dev) -> None:
 
 
 PROFILE_CASES = ("self_cfg2", "self_cfg1", "prologue_cfg2", "head_norm_cfg3", "cross_cfg3",
-                 "cross_b2_512", "rowquant_cfg3", "prologue_bwd_cfg5", "vae_d384")
+                 "cross_b2_512", "rowquant_cfg3", "prologue_bwd_cfg5", "vae_d384", "qkv_proj_cfg2",
+                 "xq_proj_cfg3", "xkv_proj_cfg3")
 
 
 def profile_case(name: str, steps: int, pkg, fp8, dev) -> dict:
@@ -175,6 +176,23 @@ def profile_case(name: str, steps: int, pkg, fp8, dev) -> dict:
         else:
             o_att = torch.randn(2, S, H * d, generator=g).to(dev, BF)
             fn = lambda: fp8.rowquant(o_att)
+    elif name in ("qkv_proj_cfg2", "xq_proj_cfg3", "xkv_proj_cfg3"):
+        proj = importlib.import_module("anima_flat_amd.kernels.proj")
+        p = prologue_qkv(pkg, B, S, H, 1002, dev)
+        D = H * d
+        if name == "qkv_proj_cfg2":
+            hid = torch.randn(B, S, D, generator=g).to(dev, BF)
+            wq = (torch.randn(3 * D, D, generator=g) * D**-0.5).to(dev, BF)
+            fn = lambda: proj.qkv_proj_norm_rope(hid, wq, p["q_weight"], p["k_weight"], p["cos"], p["sin"], H, eps)
+        elif name == "xq_proj_cfg3":
+            hx = torch.randn(2, S, D, generator=g).to(dev, BF)
+            wx = (torch.randn(D, D, generator=g) * D**-0.5).to(dev, BF)
+            fn = lambda: proj.proj_head_norm(hx, wx, p["q_weight"], H, eps)
+        else:
+            ctx_t = torch.randn(2, 512, 1024, generator=g).to(dev, BF)
+            wkv = (torch.randn(2 * D, 1024, generator=g) * 1024**-0.5).to(dev, BF)
+            kw16 = p["k_weight"].to(BF)
+            fn = lambda: proj.kv_proj_norm(ctx_t, wkv, kw16, H, eps)
     elif name == "vae_d384":
         vae = importlib.import_module("anima_flat_amd.vae")
         qv, kv_, vv = (torch.randn(1, 1, 16384, 384, generator=g).to(dev, BF) for _ in range(3))
@@ -448,6 +466,35 @@ def main() -> int:
                 "what": "qkv_proj_norm_rope vs F.linear (hipBLASLt) + qkv_norm_rope, B=1, 4096 tokens",
             }
             del hid, wq
+
+            # Cross-attention projections at config 3 (B=2, 4096 image tokens,
+            # 512 text tokens of width 1024): xq + head_norm and xkv + the key
+            # RMSNorm, fused vs torch's GEMM + the separate normalisation.
+            hx = torch.randn(2, S, H * d, device=dev, dtype=BF)
+            wx = (torch.randn(H * d, H * d, device=dev) * (H * d) ** -0.5).to(BF)
+            ctx_t = torch.randn(2, 512, 1024, device=dev, dtype=BF)
+            wkv = (torch.randn(2 * H * d, 1024, device=dev) * 1024**-0.5).to(BF)
+            kw16 = p["k_weight"].to(BF)
+            xq_fused = lambda: proj.proj_head_norm(hx, wx, p["q_weight"], H, eps)
+            xq_split = lambda: pkg.head_norm(torch.nn.functional.linear(hx, wx), p["q_weight"], H, eps)
+
+            def xkv_split():
+                kk, vv = torch.nn.functional.linear(ctx_t, wkv).view(2, 512, 2, H, d).unbind(2)
+                return torch.nn.functional.rms_norm(kk, (d,), kw16, eps).contiguous(), vv.contiguous()
+
+            xkv_fused = lambda: proj.kv_proj_norm(ctx_t, wkv, kw16, H, eps)
+            prewarm(xq_fused, 0.2)
+            for key, fu, sp, flops, what in (
+                ("xq_proj_cfg3", xq_fused, xq_split, 2 * 2 * S * (H * d) ** 2,
+                 "proj_head_norm vs F.linear (hipBLASLt) + head_norm, B=2, 4096 tokens, K=2048"),
+                ("xkv_proj_cfg3", xkv_fused, xkv_split, 2 * 2 * 512 * 1024 * 2 * H * d,
+                 "kv_proj_norm vs F.linear + F.rms_norm (+ contiguous k, v), B=2, 512 tokens, K=1024"),
+            ):
+                us_f, us_s = time_graph(fu), time_graph(sp)
+                extras[key] = {"fused_us": round(us_f * 1e3, 2),
+                               "fused_TFLOP/s": round(flops / (us_f * 1e-3) / 1e12, 1),
+                               "unfused_us": round(us_s * 1e3, 2), "what": what}
+            del hx, wx, ctx_t, wkv
 
         # Config 5: forward + backward (LoRA training attention), B=1, 4096.
         qg, kg, vg = (t.detach().clone().requires_grad_(True) for t in (q, k, v.contiguous()))

@@ -101,6 +101,35 @@ int aa_qkv_proj_norm_rope(const void* hid, int64_t hid_row_stride, const void* w
                           float eps, int dtype, void* stream);
 
 /*
+ * A projection fused with per-head RMSNorm: y = aa_head_norm_fwd of
+ * x @ weight^T (bf16), the projection never reaching memory.
+ *   x [B*S rows, K], row r at x + r * x_row_stride elements (x_row_stride >= K,
+ *   a multiple of 8; K a multiple of 32); weight [H*hd, K] contiguous (nn.Linear
+ *   layout, no bias); y [B, S, H, hd] contiguous; norm_weight [hd] float32.
+ * Replaces: src/model.py:324 (b.xq(hid), model.py:138, followed by head_norm,
+ *           src/kernels/rope.py:648-652) on the inference path.
+ */
+int aa_proj_head_norm(const void* x, int64_t x_row_stride, const void* weight, int64_t K,
+                      void* y, const float* norm_weight,
+                      int64_t B, int64_t S, int64_t H, int64_t hd,
+                      float eps, int dtype, void* stream);
+
+/*
+ * The context's keys and values with the key-side RMSNorm fused:
+ * kv = ctx @ weight^T (bf16, [B, S, 2, H, hd]), k = RMSNorm(kv[:, :, 0]) with
+ * k_weight, v = kv[:, :, 1], kv never reaching memory.
+ *   ctx [B*S rows, K] as x above; weight [2*H*hd, K] contiguous; k, v
+ *   [B, S, H, hd] contiguous; k_weight [hd] float32 (pass the bf16 weight
+ *   widened, as F.rms_norm applies it in the activation dtype).
+ * Replaces: src/model.py:256-258 (b.xkv(ctx), model.py:139, .view().unbind(),
+ *           F.rms_norm of k) in encode_context, inference path.
+ */
+int aa_kv_proj_norm(const void* ctx, int64_t ctx_row_stride, const void* weight, int64_t K,
+                    void* k, void* v, const float* k_weight,
+                    int64_t B, int64_t S, int64_t H, int64_t hd,
+                    float eps, int dtype, void* stream);
+
+/*
  * Per-head RMSNorm: x [B, S, H*hd] contiguous -> y [B, S, H, hd] contiguous.
  * Replaces: src/kernels/rope.py:203-212 (_head_norm), kernel rope.py:146-172.
  */

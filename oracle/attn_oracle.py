@@ -121,6 +121,31 @@ def head_norm(
     return rms_norm_heads(x.to(dtype).reshape(B, S, heads, hd), weight.to(dtype), eps, round_to)
 
 
+def proj_head_norm(
+    x: torch.Tensor, weight: torch.Tensor, norm_weight: torch.Tensor, heads: int, eps: float = 1e-5
+) -> torch.Tensor:
+    """q of the cross-attention, src/model.py:324: head_norm(b.xq(hid), ...) with
+    b.xq an nn.Linear without bias (model.py:138); the projection accumulated in
+    float32 and rounded to bf16 as the GEMM writes it, then `head_norm`."""
+    y = (x.float() @ weight.float().T).to(BF16)
+    return head_norm(y.float(), norm_weight, heads, eps)
+
+
+def kv_proj_norm(
+    ctx: torch.Tensor, weight: torch.Tensor, k_weight: torch.Tensor, heads: int, eps: float = 1e-5
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-layer context keys and values, src/model.py:256-258:
+    k, v = b.xkv(ctx).view(B, S, 2, H, hd).unbind(2) (b.xkv an nn.Linear without
+    bias, model.py:139), k = F.rms_norm(k, (hd,), b.xk_norm.to(k.dtype), eps):
+    the projection rounded to bf16, the norm in float32 with the weight rounded
+    to bf16, the result rounded to bf16; v as projected."""
+    B, S, _ = ctx.shape
+    hd = k_weight.numel()
+    kv = (ctx.float() @ weight.float().T).to(BF16).float().view(B, S, 2, heads, hd)
+    k = rms_norm_heads(kv[:, :, 0], k_weight.to(BF16).float(), eps)
+    return k, kv[:, :, 1]
+
+
 def qkv_norm_rope_backward(
     qkv: torch.Tensor,
     dq: torch.Tensor,

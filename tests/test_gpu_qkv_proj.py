@@ -113,3 +113,114 @@ def test_qkv_proj_deterministic(pkg, proj):
     b = _run(proj, hid, w, qw, kw, cos, sin, 16, 1e-6)
     for x, y in zip(a, b):
         assert torch.equal(x, y)
+
+
+# ------------------------------------------- cross-attention projections --
+# proj_head_norm: q = head_norm(b.xq(hid), b.xq_norm, heads, eps) (src/model.py:324).
+# kv_proj_norm: k, v = b.xkv(ctx).view(B, S, 2, H, hd).unbind(2); k = F.rms_norm(k, ...)
+# (src/model.py:256-258). Oracle: oracle.proj_head_norm / oracle.kv_proj_norm; the
+# same bar as above (normalised outputs to rel-L2 5e-3 and max-abs max(2e-2, 2^-7 max),
+# the plain projection v to one bf16 ulp on nearly every element).
+
+
+def _lin_inputs(B, S, K, N, seed):
+    g = torch.Generator().manual_seed(seed)
+    x = ref.bf16_normal((B, S, K), g)
+    w = (torch.randn(N, K, generator=g) * K**-0.5).to(BF)
+    return x, w, ref.norm_weight(128, g)
+
+
+def _normed(a, e, tag):
+    assert a.dtype == BF and a.is_contiguous() and a.shape == e.shape
+    parity(a, e.float(), max_abs=max(2e-2, e.float().abs().max().item() * 2.0**-7), name=tag)
+
+
+@pytest.mark.parametrize(
+    "B,S,H,K,eps",
+    [
+        (2, 4096, 16, 2048, 1e-6),  # config 3's query side
+        (1, 300, 3, 2048, 1e-5),  # odd head count: half-empty last column pair
+        (3, 5, 1, 96, 1e-6),  # K = 96: three k-steps, one head
+        (1, 257, 8, 1024, 1e-6),  # K != heads * head_dim
+    ],
+)
+def test_proj_head_norm_matches_oracle(pkg, proj, B, S, H, K, eps):
+    x, w, nw = _lin_inputs(B, S, K, H * 128, seed=1300 + S + H)
+    with torch.no_grad():
+        y = proj.proj_head_norm(x.to("cuda:0", BF), w.to("cuda:0"), nw.to("cuda:0"), H, eps)
+    torch.cuda.synchronize()
+    _normed(y, ref.proj_head_norm(x, w, nw, H, eps), f"proj_head_norm B{B} S{S} H{H} K{K}")
+
+
+def test_proj_head_norm_strided_equals_unfused(pkg, proj):
+    """x as a strided view; the fused result equals F.linear + head_norm on the GPU."""
+    B, S, H, K = 2, 512, 16, 2048
+    x, w, nw = _lin_inputs(B, S, K, H * 128, seed=1401)
+    dev = "cuda:0"
+    wide = torch.zeros(B, S, K + 512, dtype=BF)
+    wide[:, :, 128 : 128 + K] = x
+    view = wide.to(dev)[:, :, 128 : 128 + K]
+    with torch.no_grad():
+        y = proj.proj_head_norm(view, w.to(dev), nw.to(dev), H, 1e-6)
+        u = pkg.head_norm(torch.nn.functional.linear(x.to(dev, BF), w.to(dev)), nw.to(dev), H, 1e-6)
+    torch.cuda.synchronize()
+    _normed(y, ref.proj_head_norm(x, w, nw, H, 1e-6), "proj_head_norm strided")
+    _normed(y, u.float().cpu(), "proj_head_norm fused vs unfused")
+
+
+@pytest.mark.parametrize(
+    "B,S,H,K,eps",
+    [
+        (2, 512, 16, 1024, 1e-6),  # config 3's context: text_dim 1024, 512 tokens
+        (1, 77, 1, 1024, 1e-5),  # one head: two sections, one column pair
+        (3, 40, 5, 256, 1e-6),
+    ],
+)
+def test_kv_proj_norm_matches_oracle(pkg, proj, B, S, H, K, eps):
+    ctx, w, kw = _lin_inputs(B, S, K, 2 * H * 128, seed=1500 + S + H)
+    kw16 = kw.to(BF)  # the reference passes b.xk_norm.to(k.dtype)
+    with torch.no_grad():
+        k, v = proj.kv_proj_norm(ctx.to("cuda:0", BF), w.to("cuda:0"), kw16.to("cuda:0"), H, eps)
+    torch.cuda.synchronize()
+    ek, ev = ref.kv_proj_norm(ctx, w, kw16, H, eps)
+    _normed(k, ek, f"kv_proj_norm k B{B} S{S} H{H}")
+    assert v.dtype == BF and v.is_contiguous() and v.shape == ev.shape
+    vc = v.float().cpu()
+    ulp = (vc - ev).abs() <= ev.abs() * 2.0**-7 + 1e-30
+    assert ulp.float().mean().item() > 0.999, f"v beyond one bf16 ulp on {(~ulp).sum().item()} elements"
+
+
+def test_kv_proj_norm_equals_reference_expression(pkg, proj):
+    """Against the reference's own torch expression run on the GPU (F.linear, view,
+    unbind, F.rms_norm with the weight in the activation dtype), on a strided context."""
+    B, S, H, K = 2, 512, 16, 1024
+    ctx, w, kw = _lin_inputs(B, S, K, 2 * H * 128, seed=1601)
+    dev = "cuda:0"
+    wide = torch.zeros(B, S, K + 64, dtype=BF)
+    wide[:, :, :K] = ctx
+    view = wide.to(dev)[:, :, :K]
+    kwd = kw.to(dev)
+    with torch.no_grad():
+        k, v = proj.kv_proj_norm(view, w.to(dev), kwd.to(BF), H, 1e-6)
+        uk, uv = torch.nn.functional.linear(ctx.to(dev, BF), w.to(dev)).view(B, S, 2, H, 128).unbind(2)
+        uk = torch.nn.functional.rms_norm(uk, (128,), kwd.to(uk.dtype), 1e-6)
+    torch.cuda.synchronize()
+    _normed(k, uk.float().cpu(), "kv_proj_norm k vs torch")
+    _normed(v, uv.float().cpu(), "kv_proj_norm v vs torch")
+
+
+def test_cross_projections_reject_bad_inputs(pkg, proj):
+    dev = "cuda:0"
+    x = torch.zeros(1, 8, 256, dtype=BF, device=dev)
+    nw = torch.ones(128, device=dev)
+    with pytest.raises(ValueError, match="weight"):
+        proj.proj_head_norm(x, torch.zeros(256, 128, dtype=BF, device=dev), nw, 2)
+    with pytest.raises(ValueError, match="weight"):
+        proj.kv_proj_norm(x, torch.zeros(256, 256, dtype=BF, device=dev), nw, 2)
+    with pytest.raises(ValueError, match="head_dim"):
+        proj.proj_head_norm(x, torch.zeros(128, 256, dtype=BF, device=dev), nw[:64], 2)
+    w = torch.zeros(256, 256, dtype=BF, device=dev)
+    with pytest.raises(RuntimeError, match="backward"):
+        proj.proj_head_norm(x.clone().requires_grad_(True), w, nw, 2)
+    with pytest.raises(RuntimeError, match="backward"):
+        proj.kv_proj_norm(x.clone().requires_grad_(True), torch.zeros(512, 256, dtype=BF, device=dev), nw, 2)
