@@ -115,6 +115,8 @@ void set_error(const std::string& msg);
 void clear_error();
 int fail(int code, const std::string& msg);
 int check_launch(const char* what);
+// Compute units of the current device; 0 if it cannot be queried.
+int device_cu_count();
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 

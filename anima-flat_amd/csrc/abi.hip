@@ -1,4 +1,6 @@
 // Library-wide C ABI entry points: version and per-thread error reporting.
+#include <atomic>
+
 #include "aa_common.h"
 
 namespace aa {
@@ -21,6 +23,19 @@ int check_launch(const char* what) {
     return fail(AA_EHIP, std::string(what) + ": " + hipGetErrorString(e));
   }
   return AA_OK;
+}
+
+// Compute units of the current device (queried once per device).
+int device_cu_count() {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int> cached[kMaxDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n > 0) return n;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  cached[dev].store(n, std::memory_order_relaxed);
+  return n;
 }
 
 }  // namespace aa

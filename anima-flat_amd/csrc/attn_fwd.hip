@@ -547,19 +547,6 @@ static bool stride_ok(const int64_t* s) {
 
 using namespace aa;
 
-// Compute units of the current device (queried once per device).
-static int device_cu_count() {
-  constexpr int kMaxDevices = 64;
-  static std::atomic<int> cached[kMaxDevices];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
-  int n = cached[dev].load(std::memory_order_relaxed);
-  if (n > 0) return n;
-  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-  cached[dev].store(n, std::memory_order_relaxed);
-  return n;
-}
-
 // Key split of the work items of a partial last round. With T work items
 // on ncu CUs, the last T % ncu items would run alone on under half the chip;
 // when that is so, each of them is split into nsplit key ranges (up to 8, at

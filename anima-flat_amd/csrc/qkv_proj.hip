@@ -1,33 +1,45 @@
-// Fused QKV projection + QK-RMSNorm + rotate-half RoPE: q, k, v straight
-// from the hidden states and the projection weight, one launch.
+// Fused input projections of the attention block: a bf16 GEMM whose output
+// tile is normalised (and rotated) on chip before it is stored.
 //
-// The reference computes qkv = hid @ W^T (nn.Linear without bias, bf16 out,
-// src/model.py:134,308-316) and then qkv_norm_rope on it (rope.py:616-645),
-// a 3 * H * 128 * 2-byte round trip per token through HBM between the two.
-// Here the projection's output tile never leaves the chip:
+// The reference computes the projection with nn.Linear (no bias, bf16 out)
+// and then normalises it in a second kernel, a round trip of the projection
+// output through HBM:
+//   qkv = b.qkv(hid); q, k, v = qkv_norm_rope(qkv, ...)   (src/model.py:308-316)
+//   q = head_norm(b.xq(hid), ...)                          (src/model.py:324)
+//   k, v = b.xkv(ctx).unbind(...); k = F.rms_norm(k, ...)  (src/model.py:256-258)
+// Here acc = X[MT x K] . W[NS 128 x K]^T in fp32 on v_mfma_f32_32x32x16_bf16,
+// rounded to bf16 (the value the reference's GEMM writes), staged in LDS, then
+// per token and 128-column section: RMSNorm (+ rotate-half RoPE) with the
+// prologue's math (norm_rotate) or a copy, and 256-byte row stores.
 //
-//   out tile = 256 tokens x 256 columns = two (q | k | v, head) sections of
-//   256 tokens; acc = X[256 x K] . W[256 x K]^T in fp32 on
-//   v_mfma_f32_32x32x16_bf16, rounded to bf16 (the value the reference's GEMM
-//   writes), staged in LDS, then per token RMSNorm + rotation (norm_rotate,
-//   the prologue's math) for q and k, a copy for v, and 256-byte row stores
-//   into q, k, v [ntok, H, 128].
+// Main loop: waves of 64 tokens x WN columns (2 x WN/32 accumulators), over K
+// in stages of 64: the stage's X and W rows move L2 -> LDS by DMA
+// (global_load_lds_dwordx4, no registers) into a ring of two stages, one
+// ahead, one barrier per stage. Each DMA instruction moves 8 rows x 128 bytes,
+// whole cache lines: with 16 rows x 64 bytes (half lines) per instruction the
+// same loads stream at well under half the rate, which bounded this kernel.
+// A stage in LDS is blocks of 8 rows x 64 k (1 KiB, one DMA instruction);
+// element (r, k) at (r >> 3) * 512 + (r & 7) * 64 + ((k >> 3) ^ f(r)) * 8
+// + (k & 7) with f(r) = (r & 7) ^ ((r >> 3) & 1). The XOR places the 16-byte
+// chunk an operand read takes from 16 consecutive rows in 16 distinct
+// (row parity, slot) pairs, i.e. 16 distinct bank groups: conflict-free.
 //
-// Main loop: 8 waves, each 64 tokens x one 128-column section (2 x 4
-// accumulators: 6 operand reads per 8 MFMAs), over K in stages of 32: the
-// stage's X and W rows (2 x 256 x 64 B) move HBM -> LDS by DMA
-// (global_load_lds_dwordx4, no registers) into a 4-stage ring, three stages
-// ahead, one barrier per stage. Tiles in LDS use the row-tile format of the
-// attention kernels with 32-wide rows: element (r, k) at (r >> 4) * 512
-// + (k >> 3) * 128 + (r & 15) * 8 + (k & 7), so an operand read (16 lanes on
-// one 16-byte chunk of 16 consecutive rows) covers 256 contiguous bytes and
-// one DMA instruction fills one 16-row group.
+// Tile shapes (ProjTile): 256 x 2 sections (8 waves of 64 x 128), 256 x 3
+// sections (8 waves of 64 x 192: 8 operand reads per 12 MFMAs) and 128 x 1
+// section (4 waves of 64 x 64, two workgroups per CU, for small token
+// counts). The host picks the shape with the least work on the busiest CU
+// (whole rounds of workgroups over the chip), so a projection fills the chip
+// in whole rounds where it can. Every shape accumulates each output in the
+// same order (16 k per MFMA, in increasing k), so all give identical bits.
 //
 // Work order: workgroups go to XCDs in contiguous ranges (xcd_remap), and
-// within the range in groups of 4 token tiles x all column tiles, so the 32
-// workgroups an XCD runs at once share 4 X tiles and 8 W tiles in its L2.
-// With an odd number of sections (3 H) the last column tile holds one.
+// within the range in groups of 4 token tiles x all column tiles, so the
+// workgroups an XCD runs at once share a few X and W tiles in its L2. The
+// last column tile may hold fewer sections.
+#include <algorithm>
+#include <cstdlib>
 #include <string>
+#include <type_traits>
 
 #include "aa_common.h"
 #include "norm_rope.h"
@@ -35,14 +47,38 @@
 
 namespace aa {
 
-constexpr int kPM = 256;                            // tokens per workgroup
-constexpr int kPN = 256;                            // output columns: two sections
-constexpr int kPK = 32;                             // K per stage
-constexpr int kPStages = 4;
-constexpr int kPThreads = 512;
-constexpr int kPXElems = kPM * kPK;                 // 16 KiB
-constexpr int kPStageElems = kPXElems + kPN * kPK;  // + 16 KiB of W
-constexpr int kPGroupM = 4;                         // token tiles per work-order group
+constexpr int kPK = 64;       // K per stage
+constexpr int kPKMin = 32;    // K granularity: a last stage may hold 32
+constexpr int kPGroupM = 4;   // token tiles per work-order group
+
+template <int MT, int NS, int WN, int PS>
+struct ProjTile {
+  static constexpr int kMT = MT;                       // tokens per workgroup
+  static constexpr int kNS = NS;                       // sections per workgroup
+  static constexpr int kN = NS * kHd;                  // columns per workgroup
+  static constexpr int kWN = WN;                       // columns per wave
+  static constexpr int kWaves = (MT / 64) * (kN / WN);
+  static constexpr int kThreads = 64 * kWaves;
+  static constexpr int kXElems = MT * kPK;
+  static constexpr int kStageElems = (MT + kN) * kPK;
+  static constexpr int kBlocks = (MT + kN) / 8;        // 8-row DMA blocks per stage
+  static constexpr int kBPW = kBlocks / kWaves;        // ... per wave
+  static constexpr int kCB = WN / 32;                  // 32-column blocks per wave
+  static constexpr int kRingElems = 2 * kStageElems;
+  // Sections staged per epilogue pass (the ring holds the staged bf16 tiles).
+  static constexpr int kPassSecs = PS;
+  static_assert(MT % 64 == 0 && kN % WN == 0 && WN % 32 == 0, "wave tiling");
+  static_assert(kBlocks % kWaves == 0 && kBPW % 2 == 0, "DMA blocks split evenly, in pairs");
+  static_assert(PS >= 1 && PS <= NS && PS * MT * kHd <= kRingElems, "staging");
+  static_assert(kRingElems * 2 <= 160 * 1024, "LDS");
+};
+
+// The last argument is the sections staged per epilogue pass. TileB stages
+// one at a time: with two, a wave whose columns straddle the passes keeps
+// 128 accumulators live through the first pass's normalisation and spills.
+using TileA = ProjTile<256, 2, 128, 2>;  // 128 KiB ring
+using TileB = ProjTile<256, 3, 192, 1>;  // 160 KiB ring
+using TileC = ProjTile<128, 1, 64, 1>;   // 64 KiB ring, two workgroups per CU
 
 // The projection's output columns are nseg segments of H sections of 128:
 // segment g goes to out[g] ([ntok, H, 128]), RMS-normalised with weight nw[g]
@@ -68,25 +104,30 @@ struct ProjParams {
   float eps;
 };
 
-// DMA of row group g (16 rows x 32 k, 1 KiB) of a tile whose row 0 is at
-// `base` (row stride rs elements, already offset to the stage's k): lane
-// moves chunk lane >> 4 of row 16 g + (lane & 15). Rows at or past `nrows`
-// re-read row nrows - 1 (their results are not stored).
-__device__ __forceinline__ void dma_proj_group(const bf16* base, int64_t rs, int nrows,
-                                               bf16* tile, int g, int lane) {
-  const int row = min(16 * g + (lane & 15), nrows - 1);
-  dma16_off<0>(base + (int64_t)row * rs + 8 * (lane >> 4), tile + g * 512);
+// DMA of 16 bytes per lane from sbase + voff (sbase wave-uniform, held in
+// SGPRs: the per-lane address is one 32-bit offset) to LDS at lds_dst + 16 lane.
+__device__ __forceinline__ void dma16_sv(const void* sbase, uint32_t voff, const void* lds_dst) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void*)lds_dst);
+  // readfirstlane returns int: widen each half through uint32_t (a signed
+  // int would sign-extend the low half into the high one).
+  const uint64_t sb = (uint64_t)(uintptr_t)sbase;
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)sb);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(sb >> 32));
+  const uint64_t sbu = ((uint64_t)hi << 32) | (uint64_t)lo;
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbu), "s"(m0)
+               : "memory", "m0");
 }
 
-__global__ __launch_bounds__(kPThreads) void qkv_proj_kernel(ProjParams p) {
-  __shared__ __attribute__((aligned(16))) bf16 lds[kPStages * kPStageElems];
+template <class T>
+__global__ __launch_bounds__(T::kThreads) void qkv_proj_kernel(ProjParams p) {
+  __shared__ __attribute__((aligned(16))) bf16 lds[T::kRingElems];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
-  // Tile of this workgroup: token tile mt, sections 2 nt and 2 nt + 1.
+  // Tile of this workgroup: token tile mt, sections NS nt .. NS nt + NS - 1.
   const int nsec = p.nseg * p.H;
-  const int ntn = (nsec + 1) / 2;
+  const int ntn = (nsec + T::kNS - 1) / T::kNS;
   const int total = p.mtiles * ntn;
   const int L = xcd_remap(blockIdx.x, total);
   const int group = L / (kPGroupM * ntn);
@@ -95,125 +136,171 @@ __global__ __launch_bounds__(kPThreads) void qkv_proj_kernel(ProjParams p) {
   const int mt = group * kPGroupM + within % gm;
   const int nt = within / gm;
 
-  const int64_t row0 = (int64_t)mt * kPM;
-  const int nrows = (int)min<int64_t>(kPM, p.ntok - row0);
-  const int ncols = min(kPN, (nsec - 2 * nt) * kHd);
+  const int64_t row0 = (int64_t)mt * T::kMT;
+  const int nrows = (int)min<int64_t>(T::kMT, p.ntok - row0);
+  const int ncols = min(T::kN, (nsec - T::kNS * nt) * kHd);
   const bf16* xbase = p.x + row0 * p.xs;
-  const bf16* wbase = p.w + (int64_t)nt * kPN * p.K;
+  const bf16* wbase = p.w + (int64_t)nt * T::kN * p.K;
 
-  // Stage s -> ring slot s % 4; wave w moves X and W row groups 2w, 2w + 1.
+  // DMA lane roles: row (lane >> 3) of an 8-row block, LDS slot lane & 7,
+  // which holds chunk slot ^ f(row); f's second term is the block's parity,
+  // and a wave's blocks come in (even, odd) pairs.
+  const int drow = lane >> 3;
+  const int dchunk0 = (lane & 7) ^ drow;  // even blocks
+  const int dchunk1 = dchunk0 ^ 1;        // odd blocks
+
+  // Stage s -> ring slot s & 1: MT / 8 X blocks then kN / 8 W blocks,
+  // contiguous (block b at b * 512); wave w moves blocks w G .. w G + G - 1.
+  // A last stage of 32 k (K % 64 == 32) loads chunks 4..7 from chunks 0..3
+  // (in bounds; those products are not computed).
   auto issue = [&](int s) {
-    bf16* st = lds + (s % kPStages) * kPStageElems;
+    bf16* st = lds + (s & 1) * T::kStageElems;
     const int k0 = s * kPK;
-    dma_proj_group(xbase + k0, p.xs, nrows, st, 2 * wave, lane);
-    dma_proj_group(xbase + k0, p.xs, nrows, st, 2 * wave + 1, lane);
-    dma_proj_group(wbase + k0, p.K, ncols, st + kPXElems, 2 * wave, lane);
-    dma_proj_group(wbase + k0, p.K, ncols, st + kPXElems, 2 * wave + 1, lane);
+    const int cmask = p.K - k0 >= kPK ? 7 : 3;
+#pragma unroll
+    for (int i = 0; i < T::kBPW; ++i) {
+      // Wave-uniform: block b, its first row b0 (clamped), the source matrix.
+      const int b = wave * T::kBPW + i;
+      const bool is_x = b < T::kMT / 8;
+      const int last = (is_x ? nrows : ncols) - 1;
+      const int b0 = min(8 * (is_x ? b : b - T::kMT / 8), last);
+      const int64_t rs = is_x ? p.xs : (int64_t)p.K;
+      const bf16* sbase = (is_x ? xbase : wbase) + b0 * rs + k0;
+      const uint32_t voff = (uint32_t)(min(drow, last - b0) * rs +
+                                       8 * (((i & 1) ? dchunk1 : dchunk0) & cmask)) * 2;
+      dma16_sv(sbase, voff, st + b * 512);
+    }
   };
 
-  const int nk = p.K / kPK;
+  const int nk = (p.K + kPK - 1) / kPK;
+  const int nfull = p.K / kPK;  // stages of 64 k; a last one of 32 when K % 64 == 32
   issue(0);
-  if (nk > 1) issue(1);
-  if (nk > 2) issue(2);
 
-  const int wm = wave & 3;   // tokens 64 wm .. 64 wm + 63
-  const int wn = wave >> 2;  // section 2 nt + wn: columns 128 wn .. 128 wn + 127
+  constexpr int kWavesM = T::kMT / 64;
+  const int wm = wave % kWavesM;  // tokens 64 wm .. 64 wm + 63
+  const int wn = wave / kWavesM;  // columns WN wn .. WN wn + WN - 1
   const int li = lane & 31;
   const int hh = lane >> 5;
-  // Row 32 t + li of a row block, chunk 2 kk + hh: rd + 1024 t + 256 kk.
-  const int rd = (li >> 4) * 512 + (li & 15) * 8 + hh * 128;
+  // Operand read of rows R + li (R a multiple of 32), k-step kk (16 k):
+  // chunk 2 kk + hh of row li, at (R >> 3) * 512 + (kbase ^ 16 kk) with
+  // kbase = (li >> 3) * 512 + (li & 7) * 64 + (hh ^ f(li)) * 8.
+  const int kbase = (li >> 3) * 512 + (li & 7) * 64 + (hh ^ (li & 7) ^ ((li >> 3) & 1)) * 8;
 
-  f32x16 acc[4][2];
+  f32x16 acc[T::kCB][2];
 #pragma unroll
-  for (int c = 0; c < 4; ++c)
+  for (int c = 0; c < T::kCB; ++c)
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[c][t][e] = 0.f;
 
-  for (int s = 0; s < nk; ++s) {
-    // This wave's DMAs of stage s are done once at most those of the stages
-    // after it (4 each) are outstanding; the barrier then publishes every
-    // wave's and retires all reads of stage s - 1, whose slot the DMA of
-    // stage s + 3 reuses.
-    if (s + 2 < nk) {
-      asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-    } else if (s + 1 < nk) {
-      asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
-    } else {
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    }
+  // One stage of NSTEPS k-steps. Operands of kPre k-steps are read ahead of
+  // their MFMAs: those of the first kPre steps before the next DMA goes out
+  // (its asm is a compiler memory barrier, so they cannot sink to their
+  // MFMAs, and its issue time does not delay the stage's first MFMA), the
+  // rest kPre steps ahead. With 192 accumulator registers (kCB = 6) only one
+  // k-step's operands fit beside them at two waves per SIMD.
+  constexpr int kPre = T::kCB <= 4 ? 2 : 1;
+  auto stage = [&](int s, auto nsteps) {
+    constexpr int NSTEPS = decltype(nsteps)::value;
+    // This wave's DMAs of stage s are done; the barrier publishes every
+    // wave's and retires all reads of stage s - 1, whose slot stage s + 1
+    // reuses.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    if (s + 3 < nk) issue(s + 3);
-    const bf16* xs = lds + (s % kPStages) * kPStageElems + wm * 2048 + rd;
-    const bf16* ws = lds + (s % kPStages) * kPStageElems + kPXElems + wn * 4096 + rd;
+    const bf16* stg = lds + (s & 1) * T::kStageElems;
+    const bf16* xs = stg + wm * 4096;
+    const bf16* ws = stg + T::kXElems + wn * (T::kWN / 8) * 512;
+    bf16x8 a[NSTEPS][T::kCB], b[NSTEPS][2];
+    auto read = [&](int kk) {
+      const int ko = kbase ^ (16 * kk);
 #pragma unroll
-    for (int kk = 0; kk < kPK / 16; ++kk) {
-      bf16x8 a[4], b[2];
+      for (int c = 0; c < T::kCB; ++c) a[kk][c] = *reinterpret_cast<const bf16x8*>(ws + 2048 * c + ko);
 #pragma unroll
-      for (int c = 0; c < 4; ++c) a[c] = *reinterpret_cast<const bf16x8*>(ws + 1024 * c + 256 * kk);
+      for (int t = 0; t < 2; ++t) b[kk][t] = *reinterpret_cast<const bf16x8*>(xs + 2048 * t + ko);
+    };
 #pragma unroll
-      for (int t = 0; t < 2; ++t) b[t] = *reinterpret_cast<const bf16x8*>(xs + 1024 * t + 256 * kk);
+    for (int kk = 0; kk < kPre && kk < NSTEPS; ++kk) read(kk);
+    if (s + 1 < nk) issue(s + 1);
 #pragma unroll
-      for (int c = 0; c < 4; ++c)
+    for (int kk = 0; kk < NSTEPS; ++kk) {
+      if constexpr (kPre > 1) {
+        if (kk + kPre < NSTEPS) read(kk + kPre);
+      }
 #pragma unroll
-        for (int t = 0; t < 2; ++t) acc[c][t] = mfma32(a[c], b[t], acc[c][t]);
-    }
-  }
-  __syncthreads();  // every wave is done with the ring: reuse it as the output tiles
-
-  // acc[c][t] holds out^T: lane li is token 64 wm + 32 t + li, element e is
-  // column 32 c + 8 (e / 4) + 4 hh + (e % 4) of section wn. Staged as bf16
-  // rows of 128 columns per section, 16-byte chunk ch of row r at
-  // r * 128 + ((ch ^ (r & 15)) * 8).
-  bf16* mine = lds + wn * (kPM * kHd);
+      for (int c = 0; c < T::kCB; ++c)
 #pragma unroll
-  for (int c = 0; c < 4; ++c)
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int r = 64 * wm + 32 * t + li;
-#pragma unroll
-      for (int e4 = 0; e4 < 4; ++e4) {
-        const int ch = 4 * c + e4;
-        u32x2 w2;
-        w2[0] = pack_bf16(acc[c][t][4 * e4], acc[c][t][4 * e4 + 1]);
-        w2[1] = pack_bf16(acc[c][t][4 * e4 + 2], acc[c][t][4 * e4 + 3]);
-        *reinterpret_cast<u32x2*>(mine + r * 128 + ((ch ^ (r & 15)) * 8) + 4 * hh) = w2;
+        for (int t = 0; t < 2; ++t) acc[c][t] = mfma32(a[kk][c], b[kk][t], acc[c][t]);
+      if constexpr (kPre == 1) {
+        __builtin_amdgcn_sched_barrier(0);
+        if (kk + 1 < NSTEPS) read(kk + 1);
       }
     }
-  __syncthreads();
+  };
+  for (int s = 0; s < nfull; ++s) stage(s, std::integral_constant<int, kPK / 16>{});
+  if (nk > nfull) stage(nfull, std::integral_constant<int, kPKMin / 16>{});
 
-  // Per (token, section): RMSNorm + rotation (q, k) or a copy (v), 8 lanes
-  // per item, two 16-byte chunks per lane, 256-byte rows out.
+  // acc[c][t] holds out^T: lane li is token 64 wm + 32 t + li, element e is
+  // tile column WN wn + 32 c + 8 (e / 4) + 4 hh + (e % 4). Staged per pass of
+  // kPassSecs sections as bf16 rows of 128 columns per section, 16-byte chunk
+  // ch of row r at r * 128 + ((ch ^ (r & 15)) * 8).
   const int j = tid & 7;
   const int grp = tid >> 3;
   const int nmine = ncols / kHd;
-  for (int sc = 0; sc < nmine; ++sc) {
-    const int gsec = 2 * nt + sc;
-    const int seg = gsec / p.H;
-    const int head = gsec - seg * p.H;
-    bf16* out = p.out[seg];
-    const float* nw = p.nw[seg];
-    const bool rope = p.rope[seg] != 0;
-    const bf16* tile = lds + sc * (kPM * kHd);
-    for (int r = grp; r < nrows; r += kPThreads / 8) {
-      const u32x4 ra = *reinterpret_cast<const u32x4*>(tile + r * 128 + ((j ^ (r & 15)) * 8));
-      const u32x4 rb =
-          *reinterpret_cast<const u32x4*>(tile + r * 128 + (((8 + j) ^ (r & 15)) * 8));
-      const int64_t token = row0 + r;
-      bf16* dst = out + (token * p.H + head) * kHd;
-      if (!nw) {
-        st16_nt(dst + 8 * j, ra);
-        st16_nt(dst + kHalf + 8 * j, rb);
-      } else {
-        Section x;
-        unpack8(ra, x.a);
-        unpack8(rb, x.b);
-        float oa[8], ob[8];
-        if (rope) norm_rotate<true>(x, nw, p.cos, p.sin, token % p.S, j, p.eps, oa, ob);
-        else norm_rotate<false>(x, nw, nullptr, nullptr, 0, j, p.eps, oa, ob);
-        st16_nt(dst + 8 * j, pack8(oa));
-        st16_nt(dst + kHalf + 8 * j, pack8(ob));
+#pragma unroll
+  for (int p0 = 0; p0 < T::kNS; p0 += T::kPassSecs) {
+    __syncthreads();  // the ring (or the previous pass's tiles) is free
+#pragma unroll
+    for (int c = 0; c < T::kCB; ++c) {
+      const int col = T::kWN * wn + 32 * c;
+      const int sec = col >> 7;
+      if (sec < p0 || sec >= p0 + T::kPassSecs) continue;
+      bf16* mine = lds + (sec - p0) * (T::kMT * kHd);
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int r = 64 * wm + 32 * t + li;
+#pragma unroll
+        for (int e4 = 0; e4 < 4; ++e4) {
+          const int ch = ((col & 127) >> 3) + e4;
+          u32x2 w2;
+          w2[0] = pack_bf16(acc[c][t][4 * e4], acc[c][t][4 * e4 + 1]);
+          w2[1] = pack_bf16(acc[c][t][4 * e4 + 2], acc[c][t][4 * e4 + 3]);
+          *reinterpret_cast<u32x2*>(mine + r * 128 + ((ch ^ (r & 15)) * 8) + 4 * hh) = w2;
+        }
+      }
+    }
+    __syncthreads();
+
+    // Per (token, section): RMSNorm (+ rotation) or a copy, 8 lanes per item,
+    // two 16-byte chunks per lane, 256-byte rows out.
+    const int send = min(p0 + T::kPassSecs, nmine);
+    for (int sc = p0; sc < send; ++sc) {
+      const int gsec = T::kNS * nt + sc;
+      const int seg = gsec / p.H;
+      const int head = gsec - seg * p.H;
+      bf16* out = p.out[seg];
+      const float* nw = p.nw[seg];
+      const bool rope = p.rope[seg] != 0;
+      const bf16* tile = lds + (sc - p0) * (T::kMT * kHd);
+      for (int r = grp; r < nrows; r += T::kThreads / 8) {
+        const u32x4 ra = *reinterpret_cast<const u32x4*>(tile + r * 128 + ((j ^ (r & 15)) * 8));
+        const u32x4 rb =
+            *reinterpret_cast<const u32x4*>(tile + r * 128 + (((8 + j) ^ (r & 15)) * 8));
+        const int64_t token = row0 + r;
+        bf16* dst = out + (token * p.H + head) * kHd;
+        if (!nw) {
+          st16_nt(dst + 8 * j, ra);
+          st16_nt(dst + kHalf + 8 * j, rb);
+        } else {
+          Section x;
+          unpack8(ra, x.a);
+          unpack8(rb, x.b);
+          float oa[8], ob[8];
+          if (rope) norm_rotate<true>(x, nw, p.cos, p.sin, token % p.S, j, p.eps, oa, ob);
+          else norm_rotate<false>(x, nw, nullptr, nullptr, 0, j, p.eps, oa, ob);
+          st16_nt(dst + 8 * j, pack8(oa));
+          st16_nt(dst + kHalf + 8 * j, pack8(ob));
+        }
       }
     }
   }
@@ -227,6 +314,41 @@ using namespace aa;
 // What the epilogue does with one output segment.
 enum SegMode { kCopy = 0, kNorm = 1, kNormRope = 2 };
 
+// Tile shape for ntok tokens x nsec sections: 0 = TileA, 1 = TileB, 2 =
+// TileC, the one with the least time on the busiest CU: whole rounds of
+// workgroups over the chip (TileC runs two per CU) times the time of one
+// round. Round times measured on MI355X at K = 2048 (graph-timed): A 62 us,
+// B 99 us, C 36.5 us (two workgroups) -> weights 2.0, 3.2, 2 x 0.59. Ties go
+// to the lower index. The environment variable AA_PROJ_TILE = a, b or c
+// forces a shape (all give identical results); any other value is an error
+// (-1).
+static int pick_tile(int64_t ntok, int64_t nsec) {
+  if (const char* e = std::getenv("AA_PROJ_TILE")) {
+    if (e[0] && !e[1] && e[0] >= 'a' && e[0] <= 'c') return e[0] - 'a';
+    return -1;
+  }
+  const int64_t cus = std::max(1, device_cu_count());
+  struct Shape {
+    int64_t mt, ns, per_cu;
+    double weight;  // time of one round, per workgroup on a CU
+  } shapes[3] = {{TileA::kMT, TileA::kNS, 1, 2.0},
+                 {TileB::kMT, TileB::kNS, 1, 3.2},
+                 {TileC::kMT, TileC::kNS, 2, 0.59}};
+  int best = 0;
+  double best_cost = 0;
+  for (int i = 0; i < 3; ++i) {
+    const Shape& sh = shapes[i];
+    const int64_t wgs = (ntok + sh.mt - 1) / sh.mt * ((nsec + sh.ns - 1) / sh.ns);
+    const int64_t slots = cus * sh.per_cu;
+    const double cost = (double)((wgs + slots - 1) / slots) * sh.per_cu * sh.weight;
+    if (i == 0 || cost < best_cost) {
+      best = i;
+      best_cost = cost;
+    }
+  }
+  return best;
+}
+
 static int launch_proj(const char* what, const void* hid, int64_t hid_row_stride, const void* weight,
                        int64_t K, int nseg, void* const* outs, const float* const* nws,
                        const int* modes, const float* cos, const float* sin, int64_t B, int64_t S,
@@ -235,7 +357,7 @@ static int launch_proj(const char* what, const void* hid, int64_t hid_row_stride
   if (hd != kHd) return fail(AA_EUNSUPPORTED, "head_dim must be 128");
   if (dtype != AA_DTYPE_BF16) return fail(AA_EUNSUPPORTED, "only bf16 activations are implemented");
   if (B < 0 || S < 0 || H <= 0 || H > 64) return fail(AA_EINVAL, w + ": bad B/S/H (H <= 64)");
-  if (K <= 0 || K % kPK != 0 || K > (1 << 20))
+  if (K <= 0 || K % kPKMin != 0 || K > (1 << 20))
     return fail(AA_EUNSUPPORTED, w + ": the input width must be a positive multiple of 32");
   if (B * S == 0) return AA_OK;
   if (!hid || !weight) return fail(AA_EINVAL, w + ": null pointer");
@@ -254,8 +376,12 @@ static int launch_proj(const char* what, const void* hid, int64_t hid_row_stride
   if (!aligned16(hid) || !aligned16(weight))
     return fail(AA_EINVAL, w + ": pointers must be 16-byte aligned");
   const int64_t ntok = B * S;
-  const int64_t mtiles = (ntok + kPM - 1) / kPM;
-  const int64_t total = mtiles * ((nseg * H + 1) / 2);
+  const int tile = pick_tile(ntok, nseg * H);
+  if (tile < 0) return fail(AA_EINVAL, "AA_PROJ_TILE must be a, b or c");
+  const int64_t mt = tile == 2 ? TileC::kMT : TileA::kMT;
+  const int ns = tile == 0 ? TileA::kNS : tile == 1 ? TileB::kNS : TileC::kNS;
+  const int64_t mtiles = (ntok + mt - 1) / mt;
+  const int64_t total = mtiles * ((nseg * H + ns - 1) / ns);
   if (total > 0x7fffffff) return fail(AA_EUNSUPPORTED, w + ": too many tokens");
   ProjParams p;
   p.x = (const bf16*)hid;
@@ -275,7 +401,9 @@ static int launch_proj(const char* what, const void* hid, int64_t hid_row_stride
   p.K = (int)K;
   p.mtiles = (int)mtiles;
   p.eps = eps;
-  qkv_proj_kernel<<<dim3((unsigned)total), kPThreads, 0, st>>>(p);
+  if (tile == 0) qkv_proj_kernel<TileA><<<dim3((unsigned)total), TileA::kThreads, 0, st>>>(p);
+  else if (tile == 1) qkv_proj_kernel<TileB><<<dim3((unsigned)total), TileB::kThreads, 0, st>>>(p);
+  else qkv_proj_kernel<TileC><<<dim3((unsigned)total), TileC::kThreads, 0, st>>>(p);
   return check_launch(what);
 }
 

@@ -123,6 +123,15 @@ def test_invalid_arguments_fail_before_any_launch(pkg, lib):
     assert proj(65, 128, 0) == L.AA_EINVAL  # H > 64
     assert proj(2, 128, 0) == L.AA_EINVAL  # null pointers
     assert proj(2, 128, 0, B=0) == L.AA_OK  # no tokens: nothing to do
+    xq = lambda hd, K, B=1: lib.aa_proj_head_norm(None, 256, None, K, None, None, B, 4, 2, hd, 1e-6, 0, None)
+    assert xq(96, 256) == L.AA_EUNSUPPORTED  # head_dim
+    assert xq(128, 80) == L.AA_EUNSUPPORTED  # K % 32
+    assert xq(128, 256) == L.AA_EINVAL  # null pointers
+    assert xq(128, 256, B=0) == L.AA_OK
+    xkv = lambda K, rs=1024: lib.aa_kv_proj_norm(None, rs, None, K, None, None, None, 1, 4, 2, 128, 1e-6, 0, None)
+    assert xkv(1000) == L.AA_EUNSUPPORTED  # K % 32
+    assert xkv(1024) == L.AA_EINVAL  # null pointers
+    assert "kv_proj_norm" in lib.aa_last_error().decode()
     assert lib.aa_ctx_scale_fwd(None, None, None, None, 1, 4, 2, 128, 3, None) == L.AA_EUNSUPPORTED
     assert lib.aa_context_lengths(None, 1, 8, 8, 64, 8, 3, None, None, None, 0, None) == L.AA_EUNSUPPORTED
     assert lib.aa_context_lengths(None, 1, 8, 8, 64, 8, 2, None, None, None, 0, None) == L.AA_EINVAL

@@ -224,3 +224,61 @@ def test_cross_projections_reject_bad_inputs(pkg, proj):
         proj.proj_head_norm(x.clone().requires_grad_(True), w, nw, 2)
     with pytest.raises(RuntimeError, match="backward"):
         proj.kv_proj_norm(x.clone().requires_grad_(True), torch.zeros(512, 256, dtype=BF, device=dev), nw, 2)
+
+
+# ---------------------------------------------------------- tile shapes --
+# The launcher picks one of three workgroup tiles (256 tokens x 2 sections,
+# 256 x 3, 128 x 1) by how evenly the workgroups fill the chip; AA_PROJ_TILE
+# forces one. Every shape accumulates each output in the same order, so the
+# results must be bit-identical; the default shape is held to the oracle above.
+
+
+def _all_tiles(monkeypatch, fn):
+    outs = {}
+    for t in "abc":
+        monkeypatch.setenv("AA_PROJ_TILE", t)
+        with torch.no_grad():
+            r = fn()
+        torch.cuda.synchronize()
+        outs[t] = r if isinstance(r, tuple) else (r,)
+    monkeypatch.delenv("AA_PROJ_TILE")
+    return outs
+
+
+def _same_bits(outs, tag):
+    for t in "bc":
+        for i, (x, y) in enumerate(zip(outs["a"], outs[t])):
+            assert torch.equal(x, y), f"{tag}: tile {t} output {i} differs from tile a"
+
+
+@pytest.mark.parametrize("B,S,H", [(1, 4096, 16), (2, 300, 16), (1, 77, 2), (3, 5, 1), (1, 1100, 5)])
+def test_qkv_proj_tile_shapes_identical(pkg, proj, monkeypatch, B, S, H):
+    hid, w, qw, kw, cos, sin = _inputs(B, S, H, seed=1700 + S + H)
+    dev = "cuda:0"
+    args = (hid.to(dev, BF), w.to(dev, BF), qw.to(dev), kw.to(dev), cos.to(dev), sin.to(dev), H, 1e-6)
+    outs = _all_tiles(monkeypatch, lambda: proj.qkv_proj_norm_rope(*args))
+    _same_bits(outs, f"qkv B{B} S{S} H{H}")
+    _check(outs["b"], ref.qkv_proj_norm_rope(hid, w, qw, kw, cos, sin, H, 1e-6), f"tile b B{B} S{S} H{H}")
+
+
+@pytest.mark.parametrize("B,S,H,K", [(2, 1000, 3, 512), (1, 257, 16, 2048), (1, 31, 1, 64)])
+def test_cross_proj_tile_shapes_identical(pkg, proj, monkeypatch, B, S, H, K):
+    dev = "cuda:0"
+    x, wq, nw = _lin_inputs(B, S, K, H * 128, seed=1800 + S)
+    _, wkv, _ = _lin_inputs(B, S, K, 2 * H * 128, seed=1900 + S)
+    xd, wqd, wkvd, nwd = x.to(dev, BF), wq.to(dev), wkv.to(dev), nw.to(dev)
+    outs = _all_tiles(monkeypatch, lambda: proj.proj_head_norm(xd, wqd, nwd, H, 1e-6))
+    _same_bits(outs, f"xq B{B} S{S} H{H} K{K}")
+    _normed(outs["c"][0], ref.proj_head_norm(x, wq, nw, H, 1e-6), f"xq tile c B{B} S{S} H{H}")
+    outs = _all_tiles(monkeypatch, lambda: proj.kv_proj_norm(xd, wkvd, nwd.to(BF), H, 1e-6))
+    _same_bits(outs, f"xkv B{B} S{S} H{H} K{K}")
+    ek, _ = ref.kv_proj_norm(x, wkv, nw.to(BF), H, 1e-6)
+    _normed(outs["b"][0], ek, f"xkv tile b B{B} S{S} H{H}")
+
+
+def test_proj_tile_env_rejects_unknown_value(pkg, proj, monkeypatch):
+    dev = "cuda:0"
+    x = torch.zeros(1, 8, 256, dtype=BF, device=dev)
+    monkeypatch.setenv("AA_PROJ_TILE", "z")
+    with pytest.raises(ValueError, match="AA_PROJ_TILE"):
+        proj.proj_head_norm(x, torch.zeros(256, 256, dtype=BF, device=dev), torch.ones(128, device=dev), 2)
