@@ -127,50 +127,58 @@ __device__ __forceinline__ Item decode_item(const FwdParams& p, int it) {
   return r;
 }
 
-// K/V tile DMA of one group-A wave: K into the row tile, V into the swizzled
-// row tile (tile_io.h). A DMA instruction fills 1 KB = one 16-row group x 4
-// chunks; wave w fills blocks 4 w .. 4 w + 3, i.e. rows 16 w .. 16 w + 15 in
-// chunks lq + 4 i. Rows past klen (last tile only) re-read row klen-1: finite
-// data whose scores are masked to -inf, so their P is 0.
+// K/V tile DMA of one group-A wave into K and V line tiles (tile_io.h). A DMA
+// instruction fills one 1 KB block = 8 rows x 64 d from 8 whole 128-byte
+// lines; wave w fills blocks 4 w .. 4 w + 3: d-half w >> 1, rows
+// 32 (w & 1) + 8 i + (lane >> 3) for i = 0..3. Full tiles use a scalar row
+// base per instruction and a 32-bit per-lane offset. Rows past klen (last
+// tile only) re-read row klen-1: finite data whose scores are masked to
+// -inf, so their P is 0.
 struct KVDma {
-  int b0, krow, vrow, chunk0, koff, voff;
+  int b0, rw, rbase, kcol0, kcol1, vcol;  // rw: the wave's first row (uniform)
+  uint32_t koff0, koff1, voff;
 
   __device__ __forceinline__ void setup(const FwdParams& p, int wave, int lane) {
     b0 = wave * kDmaPerWave;
-    const int lq = lane >> 4;
-    krow = 16 * (b0 >> 2) + (lane & 15);
-    vrow = 16 * (b0 >> 2) + ((lane & 15) ^ (4 * lq));
-    chunk0 = 4 * (b0 & 3) + lq;
-    koff = krow * (int)p.ks1 + 8 * chunk0;
-    voff = vrow * (int)p.vs1 + 8 * chunk0;
+    rw = 32 * (wave & 1);
+    rbase = rw + (lane >> 3);
+    const int h64 = 64 * (wave >> 1);
+    kcol0 = h64 + 8 * line_k_chunk(lane, 0);
+    kcol1 = h64 + 8 * line_k_chunk(lane, 1);
+    vcol = h64 + 8 * line_v_chunk(lane);
+    const int r = lane >> 3;
+    koff0 = (uint32_t)(r * p.ks1 + kcol0) * 2u;
+    koff1 = (uint32_t)(r * p.ks1 + kcol1) * 2u;
+    voff = (uint32_t)(r * p.vs1 + vcol) * 2u;
   }
 
   // Tile t (keys 64 t ..) of the (batch, head) at kp / vp into kd / vd.
   __device__ __forceinline__ void issue(const FwdParams& p, const bf16* kp, const bf16* vp, int klen,
                                         int t, bf16* kd, bf16* vd) const {
     const int kb = t * kBN;
+    static_assert(kDmaPerWave == 4, "four DMA blocks per wave per tile");
     if (kb + kBN <= klen) {
-      // Chunks lq + 4 i of one row: 64-byte steps, as immediate offsets.
-      static_assert(kDmaPerWave == 4, "four DMA blocks per wave per tile");
-      const bf16* vt = vp + (int64_t)kb * p.vs1 + voff;
-      dma16_off<0>(vt, vd + b0 * 512);
-      dma16_off<64>(vt, vd + (b0 + 1) * 512);
-      dma16_off<128>(vt, vd + (b0 + 2) * 512);
-      dma16_off<192>(vt, vd + (b0 + 3) * 512);
-      const bf16* kt = kp + (int64_t)kb * p.ks1 + koff;
-      dma16_off<0>(kt, kd + b0 * 512);
-      dma16_off<64>(kt, kd + (b0 + 1) * 512);
-      dma16_off<128>(kt, kd + (b0 + 2) * 512);
-      dma16_off<192>(kt, kd + (b0 + 3) * 512);
+#pragma unroll
+      for (int i = 0; i < kDmaPerWave; ++i) {
+        const int row0 = kb + rw + 8 * i;
+        dma16_sv(vp + (int64_t)row0 * p.vs1, voff, vd + (b0 + i) * 512);
+      }
+#pragma unroll
+      for (int i = 0; i < kDmaPerWave; ++i) {
+        const int row0 = kb + rw + 8 * i;
+        dma16_sv(kp + (int64_t)row0 * p.ks1, (i & 1) ? koff1 : koff0, kd + (b0 + i) * 512);
+      }
     } else {
-      const int vr = min(kb + vrow, klen - 1);
-      const int kr = min(kb + krow, klen - 1);
 #pragma unroll
-      for (int i = 0; i < kDmaPerWave; ++i)
-        dma16(vp + (int64_t)vr * p.vs1 + 8 * (chunk0 + 4 * i), vd + (b0 + i) * 512);
+      for (int i = 0; i < kDmaPerWave; ++i) {
+        const int r = min(kb + rbase + 8 * i, klen - 1);
+        dma16(vp + (int64_t)r * p.vs1 + vcol, vd + (b0 + i) * 512);
+      }
 #pragma unroll
-      for (int i = 0; i < kDmaPerWave; ++i)
-        dma16(kp + (int64_t)kr * p.ks1 + 8 * (chunk0 + 4 * i), kd + (b0 + i) * 512);
+      for (int i = 0; i < kDmaPerWave; ++i) {
+        const int r = min(kb + rbase + 8 * i, klen - 1);
+        dma16(kp + (int64_t)r * p.ks1 + ((i & 1) ? kcol1 : kcol0), kd + (b0 + i) * 512);
+      }
     }
   }
 };
@@ -186,18 +194,22 @@ struct FwdWave {
   float l4[4];
   f32x16 s0, s1;  // S^T of the tile between its M and X blocks
   bf16x8 pb[4];   // P^T of the tile between its X block and the next M block
-  int hh, li, k_rd, v_tr0, v_tr1;
+  int hh, li;
+  int k_rd[4];  // line_k_rd(lane, j)
+  int v_tr[2];  // line_v_tr(lane, dt & 1)
   float c, thr_raw;
 
   __device__ __forceinline__ void setup(int lane, float c_) {
     li = lane & 31;
     hh = lane >> 5;
-    // K operand (kt, kk): row 32 kt + li, chunk 2 kk + hh -> k_rd + 4096 kt
-    // + 256 kk. V^T operand (dt, c4): the transposed read of the swizzled V
-    // rows (tile_io.h), keys in the order of the P^T B operands.
-    k_rd = row_rd(lane);
-    v_tr0 = swz_tr_rd(lane, 0);
-    v_tr1 = swz_tr_rd(lane, 1);
+    // K operand (kt, kk): row 32 kt + li, chunk 2 kk + hh of the K line tile
+    // -> k_rd[kk & 3] + 4096 (kk >> 2) + 2048 kt. V^T operand (dt, c4): the
+    // transposed read of the V line tile (tile_io.h), keys in the order of
+    // the P^T B operands.
+#pragma unroll
+    for (int j = 0; j < 4; ++j) k_rd[j] = line_k_rd(lane, j);
+    v_tr[0] = line_v_tr(lane, 0);
+    v_tr[1] = line_v_tr(lane, 1);
     c = c_;
     thr_raw = kRescaleThreshold / c;
   }
@@ -247,9 +259,9 @@ struct FwdWave {
     }
     bf16x8 q_ops[kPrefetch];
     auto load_op = [&](int op) -> bf16x8 {
-      if (op < 16) return read_tr_operand(vs, op >> 2, op & 3, v_tr0, v_tr1);
+      if (op < 16) return read_tr_line(vs, op >> 2, op & 3, v_tr[op & 1]);
       const int kk = (op - 16) >> 1, kt = (op - 16) & 1;
-      return *reinterpret_cast<const bf16x8*>(ks + k_rd + 4096 * kt + 256 * kk);
+      return *reinterpret_cast<const bf16x8*>(ks + k_rd[kk & 3] + 4096 * (kk >> 2) + 2048 * kt);
     };
     auto run_op = [&](int op, bf16x8 a) {
       if (op < 16) {
@@ -602,9 +614,12 @@ static int prepare(const aa_attn_fwd_args* a, FwdParams& p) {
   if (a->ln_pad && !a->seqused_k) return fail(AA_EINVAL, "attn_fwd: ln_pad needs seqused_k");
   if (!(a->softmax_scale > 0.f) || !std::isfinite(a->softmax_scale))
     return fail(AA_EINVAL, "attn_fwd: softmax_scale must be positive and finite");
-  // Per-lane DMA offsets within a 64-key tile are 32-bit.
-  if (std::llabs(a->k_stride[1]) >= (1 << 24) || std::llabs(a->v_stride[1]) >= (1 << 24))
-    return fail(AA_EUNSUPPORTED, "attn_fwd: key/value sequence stride must be < 2^24 elements");
+  // The K/V tile DMA addresses rows by a 32-bit unsigned per-lane byte
+  // offset (up to 7 rows past a scalar row base): the stride must be
+  // non-negative and small enough.
+  if (a->k_stride[1] < 0 || a->v_stride[1] < 0 || a->k_stride[1] >= (1 << 24) ||
+      a->v_stride[1] >= (1 << 24))
+    return fail(AA_EUNSUPPORTED, "attn_fwd: key/value sequence stride must be in [0, 2^24) elements");
 
   p.q = (const bf16*)a->q;
   p.k = (const bf16*)a->k;

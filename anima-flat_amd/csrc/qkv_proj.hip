@@ -104,20 +104,6 @@ struct ProjParams {
   float eps;
 };
 
-// DMA of 16 bytes per lane from sbase + voff (sbase wave-uniform, held in
-// SGPRs: the per-lane address is one 32-bit offset) to LDS at lds_dst + 16 lane.
-__device__ __forceinline__ void dma16_sv(const void* sbase, uint32_t voff, const void* lds_dst) {
-  const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void*)lds_dst);
-  // readfirstlane returns int: widen each half through uint32_t (a signed
-  // int would sign-extend the low half into the high one).
-  const uint64_t sb = (uint64_t)(uintptr_t)sbase;
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)sb);
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(sb >> 32));
-  const uint64_t sbu = ((uint64_t)hi << 32) | (uint64_t)lo;
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbu), "s"(m0)
-               : "memory", "m0");
-}
-
 template <class T>
 __global__ __launch_bounds__(T::kThreads) void qkv_proj_kernel(ProjParams p) {
   __shared__ __attribute__((aligned(16))) bf16 lds[T::kRingElems];

@@ -151,6 +151,71 @@ __device__ __forceinline__ bf16x8 read_tr_operand(const bf16* tile, int c4, int 
   return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
+// Line tile (the forward's K and V) -------------------------------------------
+//
+// 64 rows x 128 d as 16 blocks of 8 rows x 64 d (1 KB): block 8 (d >> 6)
+// + (r >> 3), row r & 7 of it at 64 elements, the row's 16-byte chunk
+// ch = (d >> 3) & 7 in slot ch ^ f(r). One DMA instruction fills one block
+// from 8 rows x 128 bytes, i.e. whole cache lines; the row-tile DMA (16 rows
+// x 64 bytes, half lines) streams at well under half that rate.
+//   K, read as row operands: fk(r) = (r & 7) ^ ((r >> 3) & 1). The 16 rows of
+//     an operand read's lane group hold its chunk in 16 distinct (row parity,
+//     slot) pairs: 16 distinct bank groups.
+//   V, read transposed: fv(r) = 4 ((r >> 1) & 1). The 32 lanes of one
+//     ds_read_b64_tr_b16 read 4 rows x 4 chunks; the XOR sends rows 2 and 3
+//     of a block to the other half of the row's 8 slots, so the 32 8-byte
+//     pieces cover all 64 banks.
+
+// DMA of 16 bytes per lane from sbase + voff (sbase wave-uniform, held in
+// SGPRs: the per-lane address is one 32-bit byte offset) to LDS at
+// lds_dst + 16 lane.
+__device__ __forceinline__ void dma16_sv(const void* sbase, uint32_t voff, const void* lds_dst) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void*)lds_dst);
+  // readfirstlane returns int: widen each half through uint32_t (a signed
+  // int would sign-extend the low half into the high one).
+  const uint64_t sb = (uint64_t)(uintptr_t)sbase;
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)sb);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(sb >> 32));
+  const uint64_t sbu = ((uint64_t)hi << 32) | (uint64_t)lo;
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbu), "s"(m0)
+               : "memory", "m0");
+}
+
+// Chunk (0..7, within the block's 64 d) that DMA lane `lane` moves into its
+// slot: row (lane >> 3) of the block, slot lane & 7. blk_odd = block parity.
+__device__ __forceinline__ int line_k_chunk(int lane, int blk_odd) {
+  return (lane & 7) ^ (lane >> 3) ^ blk_odd;
+}
+__device__ __forceinline__ int line_v_chunk(int lane) {
+  return (lane & 7) ^ (4 * ((lane >> 4) & 1));
+}
+
+// Row-operand read of a K line tile: row 32 kt + li, chunk 2 kk + hh
+// (kk = 0..7) is at line_k_rd(lane, kk & 3) + 4096 (kk >> 2) + 2048 kt.
+__device__ __forceinline__ int line_k_rd(int lane, int j) {
+  const int li = lane & 31, hh = lane >> 5;
+  const int fk = (li & 7) ^ ((li >> 3) & 1);
+  return ((li >> 3) * 512 + (li & 7) * 64 + (hh ^ fk) * 8) ^ (16 * j);
+}
+
+// Transposed-read offsets of a V line tile (the pieces swz_tr_rd describes:
+// in a group of 16 lanes G = lane / 16, lanes 4 j + c address piece c of row
+// 16 c4 + 4 (G >> 1) + j + 8 r2, columns 32 dt + 16 (G & 1) + 4 c .. + 3):
+// the piece is at line_v_tr(lane, dt & 1) + 4096 (dt >> 1) + 1024 c4 + 512 r2.
+__device__ __forceinline__ int line_v_tr(int lane, int dt_odd) {
+  const int G = lane >> 4, j = (lane >> 2) & 3, c = lane & 3;
+  const int ri = 4 * (G >> 1) + j;
+  return ri * 64 + 16 * (G & 1) + 8 * (c >> 1) + 4 * (c & 1) + 32 * (dt_odd ^ ((j >> 1) & 1));
+}
+
+// Transposed operand (dt, c4) of a V line tile; tr = line_v_tr(lane, dt & 1).
+__device__ __forceinline__ bf16x8 read_tr_line(const bf16* tile, int c4, int dt, int tr) {
+  const bf16* base = tile + 4096 * (dt >> 1) + 1024 * c4 + tr;
+  const s16x4 lo = ds_read_tr(base);
+  const s16x4 hi = ds_read_tr(base + 512);
+  return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
 // Wave-private row staging -----------------------------------------------------
 //
 // 32 rows x 128 bf16 (8 KB) per wave, 16-byte chunk c of row r at element
