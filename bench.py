@@ -135,7 +135,7 @@ def copy_calibration(dev) -> None:
 
 PROFILE_CASES = ("self_cfg2", "self_cfg1", "prologue_cfg2", "head_norm_cfg3", "cross_cfg3",
                  "cross_b2_512", "rowquant_cfg3", "prologue_bwd_cfg5", "vae_d384", "qkv_proj_cfg2",
-                 "xq_proj_cfg3", "xkv_proj_cfg3")
+                 "xq_proj_cfg3", "xkv_proj_cfg3", "fwd_bwd_cfg5")
 
 
 def profile_case(name: str, steps: int, pkg, fp8, dev) -> dict:
@@ -144,6 +144,17 @@ def profile_case(name: str, steps: int, pkg, fp8, dev) -> dict:
     kernels. Inputs are the ones the headline and extras use (same shapes and seeds)."""
     B, S, H, d, eps = 1, 4096, 16, 128, 1e-6
     g = torch.Generator().manual_seed(1003)
+    if name == "fwd_bwd_cfg5":
+        p = prologue_qkv(pkg, B, S, H, 1002, dev)
+        with torch.no_grad():
+            q, k, v = pkg.qkv_norm_rope(p["qkv"], p["q_weight"], p["k_weight"], p["cos"], p["sin"], H, eps)
+        qg, kg, vg = (t.detach().clone().requires_grad_(True) for t in (q, k, v.contiguous()))
+        dout = torch.randn(B, S, H * d, device=dev, dtype=BF)
+        for _ in range(steps):
+            out = pkg.attention(qg, kg, vg)
+            torch.autograd.grad(out, (qg, kg, vg), dout)
+        torch.cuda.synchronize()
+        return {"profile_case": name, "steps": steps}
     if name in ("self_cfg2", "self_cfg1", "prologue_cfg2", "prologue_bwd_cfg5"):
         Sx, seed = (1024, 1001) if name == "self_cfg1" else (S, 1002)
         p = prologue_qkv(pkg, B, Sx, H, seed, dev)
@@ -484,7 +495,7 @@ def main() -> int:
 
             xkv_fused = lambda: proj.kv_proj_norm(ctx_t, wkv, kw16, H, eps)
             prewarm(xq_fused, 0.2)
-            for key, fu, sp, flops, what in (
+            for key, fu, sp, gflops, what in (
                 ("xq_proj_cfg3", xq_fused, xq_split, 2 * 2 * S * (H * d) ** 2,
                  "proj_head_norm vs F.linear (hipBLASLt) + head_norm, B=2, 4096 tokens, K=2048"),
                 ("xkv_proj_cfg3", xkv_fused, xkv_split, 2 * 2 * 512 * 1024 * 2 * H * d,
@@ -492,7 +503,7 @@ def main() -> int:
             ):
                 us_f, us_s = time_graph(fu), time_graph(sp)
                 extras[key] = {"fused_us": round(us_f * 1e3, 2),
-                               "fused_TFLOP/s": round(flops / (us_f * 1e-3) / 1e12, 1),
+                               "fused_TFLOP/s": round(gflops / (us_f * 1e-3) / 1e12, 1),
                                "unfused_us": round(us_s * 1e3, 2), "what": what}
             del hx, wx, ctx_t, wkv
 
