@@ -153,21 +153,29 @@ void dkdv_kernel(Params p, int nkblk, int total_blocks) {
   const int ntiles = p.ntq;
 
   // DMA by the B waves, g = wave - 4: blocks 4 g .. 4 g + 3 of the Q and dO
-  // row tiles; wave 4 also copies the stats record (9 DMA instructions per
-  // tile for wave 4, 8 for the other B waves).
+  // dual line tiles (8 rows x 128 bytes per instruction); wave 4 also copies
+  // the stats record (9 DMA instructions per tile for wave 4, 8 for the other
+  // B waves).
   const int g = wave & 3;
+  DualDma qdma, dodma;
+  qdma.setup(g, lane, p.s_q[1]);
+  dodma.setup(g, lane, p.s_do[1]);
   auto issue_tile = [&](int t) {
     const int st = t % kDkStages, q0 = t * kT, nr = min(kT, p.Sq - q0);
-    dma_row_quad_swz(qbase + (int64_t)q0 * p.s_q[1], p.s_q[1], nr, rows[st][0], g, lane);
-    dma_row_quad_swz(dobase + (int64_t)q0 * p.s_do[1], p.s_do[1], nr, rows[st][1], g, lane);
+    qdma.issue(qbase + (int64_t)q0 * p.s_q[1], p.s_q[1], nr, rows[st][0], lane);
+    dodma.issue(dobase + (int64_t)q0 * p.s_do[1], p.s_do[1], nr, rows[st][1], lane);
     if (wave == 4) dma16(statb + (int64_t)t * kStat + 4 * lane, stat[st]);
   };
 
-  // Per-lane read offsets in the swizzled row tiles (tile_io.h): row operand
-  // (hq, kk) at rs[kk & 1] + 4096 hq + 256 kk; transposed operand (c4, dt),
-  // queries in the order of the P / dZ B operands, via tb0 / tb1.
-  const int rs0 = swz_row_rd(lane, 0), rs1 = swz_row_rd(lane, 1);
-  const int tb0 = swz_tr_rd(lane, 0), tb1 = swz_tr_rd(lane, 1);
+  // Per-lane read offsets in the dual line tiles (tile_io.h): row operand
+  // (hq, kk) at rrd[kk & 3] + 4096 (kk >> 2) + 2048 hq; transposed operand
+  // (c4, dt), queries in the order of the P / dZ B operands, via trd.
+  int rrd[4], trd[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    rrd[j] = dual_row_rd(lane, j);
+    trd[j] = dual_tr_rd(lane, j >> 1, j & 1);
+  }
   const float c = p.c;
 
   f32x16 acc[4];  // dV^T (A) or dK^T (B)
@@ -204,10 +212,9 @@ void dkdv_kernel(Params p, int nkblk, int total_blocks) {
         }
     }
     auto load_op = [&](int op) -> bf16x8 {
-      if (op < 16) return read_tr_operand(tt, op >> 2, op & 3, tb0, tb1);
-      const int w = op - 16;
-      return *reinterpret_cast<const bf16x8*>(rr + ((w & 1) ? rs1 : rs0) + 4096 * (w >> 3) +
-                                               256 * (w & 7));
+      if (op < 16) return read_tr_dual(tt, op >> 2, op & 3, trd);
+      const int w = op - 16, kk = w & 7;
+      return *reinterpret_cast<const bf16x8*>(rr + rrd[kk & 3] + 4096 * (kk >> 2) + 2048 * (w >> 3));
     };
     auto run_op = [&](int op, bf16x8 a) {
       if (op < 16) {
@@ -368,19 +375,32 @@ void dq_kernel(Params p, int nqblk, int total_blocks) {
   const bf16* vbase = p.v + b * p.s_v[0] + h * p.s_v[2];
   const int ntiles = p.ntk;
 
-  // DMA by group A, g = wave: blocks 4 g .. 4 g + 3 of the K and V row tiles.
+  // DMA by group A, g = wave: blocks 4 g .. 4 g + 3 of the K and V dual line
+  // tiles (8 rows x 128 bytes per instruction). The lane offsets are computed
+  // at each issue: held in registers they would push this kernel past 256.
   const int g = wave & 3;
   auto issue_tile = [&](int t) {
     const int st = t % kDqStages, k0 = t * kT, nr = min(kT, p.Sk - k0);
-    dma_row_quad_swz(kbase + (int64_t)k0 * p.s_k[1], p.s_k[1], nr, tiles[st][0], g, lane);
-    dma_row_quad_swz(vbase + (int64_t)k0 * p.s_v[1], p.s_v[1], nr, tiles[st][1], g, lane);
+    // An opaque copy of the lane index keeps the compiler from hoisting the
+    // offsets out of the tile loop (where they would hold registers again).
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    DualDma::issue_quad(g, kbase + (int64_t)k0 * p.s_k[1], p.s_k[1], nr, tiles[st][0], ln,
+                        DualDma::lane_off(g, ln, p.s_k[1], 0), DualDma::lane_off(g, ln, p.s_k[1], 1));
+    DualDma::issue_quad(g, vbase + (int64_t)k0 * p.s_v[1], p.s_v[1], nr, tiles[st][1], ln,
+                        DualDma::lane_off(g, ln, p.s_v[1], 0), DualDma::lane_off(g, ln, p.s_v[1], 1));
   };
 
-  // Read offsets in the swizzled row tiles (tile_io.h): row operands (row
-  // 32 hk + li, chunk 2 kk + hh) at rs[kk & 1] + 4096 hk + 256 kk; transposed
-  // operands (c4, dt), keys in the order of the dZ^T B operands, via tb0 / tb1.
-  const int rs0 = swz_row_rd(lane, 0), rs1 = swz_row_rd(lane, 1);
-  const int tb0 = swz_tr_rd(lane, 0), tb1 = swz_tr_rd(lane, 1);
+  // Read offsets in the dual line tiles (tile_io.h): row operands (row
+  // 32 hk + li, chunk 2 kk + hh) at rrd[kk & 3] + 4096 (kk >> 2) + 2048 hk;
+  // transposed operands (c4, dt), keys in the order of the dZ^T B operands,
+  // via trd.
+  int rrd[4], trd[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    rrd[j] = dual_row_rd(lane, j);
+    trd[j] = dual_tr_rd(lane, j >> 1, j & 1);
+  }
   const float c = p.c;
 
   f32x16 dq[4];
@@ -416,10 +436,10 @@ void dq_kernel(Params p, int nqblk, int total_blocks) {
         }
     }
     auto load_op = [&](int op) -> bf16x8 {
-      if (op < 16) return read_tr_operand(kprev, op >> 2, op & 3, tb0, tb1);
+      if (op < 16) return read_tr_dual(kprev, op >> 2, op & 3, trd);
       const int w = op - 16, kk = w >> 2, hk = (w >> 1) & 1;
-      return *reinterpret_cast<const bf16x8*>(((w & 1) ? vr : kr) + ((kk & 1) ? rs1 : rs0) +
-                                               4096 * hk + 256 * kk);
+      return *reinterpret_cast<const bf16x8*>(((w & 1) ? vr : kr) + rrd[kk & 3] + 4096 * (kk >> 2) +
+                                               2048 * hk);
     };
     auto run_op = [&](int op, bf16x8 a) {
       if (op < 16) {
@@ -554,6 +574,11 @@ extern "C" int aa_attn_bwd(const aa_attn_bwd_args* a, void* workspace, size_t wo
                               a->out_stride,  a->dq_stride, a->dk_stride, a->dv_stride};
   for (const int64_t* s : strides)
     if (!bwd::stride_ok(s)) return fail(AA_EINVAL, "attn_bwd: strides must be multiples of 8");
+  // The tile DMA addresses rows by a 32-bit unsigned per-lane byte offset (up
+  // to 7 rows past a scalar row base).
+  for (const int64_t* s : {a->q_stride, a->dout_stride, a->k_stride, a->v_stride})
+    if (s[1] < 0 || s[1] >= (1 << 24))
+      return fail(AA_EUNSUPPORTED, "attn_bwd: q / dout / k / v sequence strides must be in [0, 2^24) elements");
   if (!(a->softmax_scale > 0.f)) return fail(AA_EINVAL, "attn_bwd: softmax_scale must be > 0");
   const bwd::WsLayout wl = bwd::ws_layout(a->B, a->Sq, a->Sk, a->H);
   const size_t need = aa_attn_bwd_workspace(a->B, a->Sq, a->Sk, a->H, a->hd);

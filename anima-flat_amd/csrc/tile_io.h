@@ -216,6 +216,93 @@ __device__ __forceinline__ bf16x8 read_tr_line(const bf16* tile, int c4, int dt,
   return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
+// Dual line tile (the backward's tiles, read both as rows and transposed):
+// the line tile's blocks with f(r) = T[r & 7] ^ 2 ((r >> 3) & 1),
+// T = 0 2 4 6 1 3 5 7. Row-operand reads: the 16 rows of a lane group hold a
+// chunk in 16 distinct (row parity, slot) pairs; transposed reads: rows 2 and
+// 3 of every 4 land in the other half of the row's slots (T differs in bit 2),
+// so the 32 lanes of a ds_read_b64_tr_b16 cover all banks.
+__device__ __forceinline__ int dual_t(int ri) {
+  return ((ri & 1) << 1) | (((ri >> 1) & 1) << 2) | ((ri >> 2) & 1);
+}
+
+// Chunk that DMA lane `lane` moves into its slot (row lane >> 3 of the block).
+__device__ __forceinline__ int dual_chunk(int lane, int blk_odd) {
+  return (lane & 7) ^ dual_t(lane >> 3) ^ (2 * blk_odd);
+}
+
+// Row operand (t, kk): row 32 t + li, chunk 2 kk + hh (kk = 0..7) at
+// dual_row_rd(lane, kk & 3) + 4096 (kk >> 2) + 2048 t.
+__device__ __forceinline__ int dual_row_rd(int lane, int j) {
+  const int li = lane & 31, hh = lane >> 5;
+  const int f = dual_t(li & 7) ^ (2 * ((li >> 3) & 1));
+  return ((li >> 3) * 512 + (li & 7) * 64 + (hh ^ f) * 8) ^ (16 * j);
+}
+
+// Transposed-read offsets (the pieces swz_tr_rd describes, rows 16 c4 +
+// 4 (G >> 1) + j + 8 r2, columns 32 dt + 16 (G & 1) + 4 c .. + 3): the piece
+// is at dual_tr_rd(lane, dt & 1, r2) + 4096 (dt >> 1) + 1024 c4 + 512 r2.
+__device__ __forceinline__ int dual_tr_rd(int lane, int dt_odd, int r2) {
+  const int G = lane >> 4, j = (lane >> 2) & 3, c = lane & 3;
+  const int ri = 4 * (G >> 1) + j;
+  const int chunk = 4 * dt_odd + 2 * (G & 1) + (c >> 1);
+  return ri * 64 + 8 * (chunk ^ dual_t(ri) ^ (2 * r2)) + 4 * (c & 1);
+}
+
+// Transposed operand (dt, c4) of a dual line tile; tr[2 p + r2] =
+// dual_tr_rd(lane, p, r2).
+__device__ __forceinline__ bf16x8 read_tr_dual(const bf16* tile, int c4, int dt, const int* tr) {
+  const bf16* base = tile + 4096 * (dt >> 1) + 1024 * c4;
+  const s16x4 lo = ds_read_tr(base + tr[2 * (dt & 1)]);
+  const s16x4 hi = ds_read_tr(base + 512 + tr[2 * (dt & 1) + 1]);
+  return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
+// DMA of one wave's quarter of a dual line tile: blocks 4 g .. 4 g + 3 =
+// d-half g >> 1, rows 32 (g & 1) + 8 i + (lane >> 3), i = 0..3. Whole tiles
+// take a scalar row base per instruction and a 32-bit per-lane byte offset;
+// a partial tile (nrows < 64, nrows >= 1) re-reads row nrows - 1 for the rows
+// past it.
+struct DualDma {
+  int g;
+  uint32_t off0, off1;  // lane_off(g, lane, rs, 0 / 1)
+
+  __device__ __forceinline__ static int col(int g, int lane, int odd) {
+    return 64 * (g >> 1) + 8 * dual_chunk(lane, odd);
+  }
+  // Per-lane byte offset from a block's first row: row lane >> 3, the chunk
+  // of an even (odd = 0) or odd block.
+  __device__ __forceinline__ static uint32_t lane_off(int g, int lane, int64_t rs, int odd) {
+    return (uint32_t)((lane >> 3) * rs + col(g, lane, odd)) * 2u;
+  }
+  __device__ __forceinline__ void setup(int g_, int lane, int64_t rs) {
+    g = g_;
+    off0 = lane_off(g, lane, rs, 0);
+    off1 = lane_off(g, lane, rs, 1);
+  }
+  __device__ __forceinline__ void issue(const bf16* base, int64_t rs, int nrows, bf16* tile,
+                                        int lane) const {
+    issue_quad(g, base, rs, nrows, tile, lane, off0, off1);
+  }
+  // The DMA itself, with the offsets given (kernels short of registers pass
+  // lane_off(...) computed at the call instead of holding them).
+  __device__ __forceinline__ static void issue_quad(int g, const bf16* base, int64_t rs, int nrows,
+                                                    bf16* tile, int lane, uint32_t o0, uint32_t o1) {
+    const int rw = 32 * (g & 1);
+    if (nrows >= kTileRows) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        dma16_sv(base + (int64_t)(rw + 8 * i) * rs, (i & 1) ? o1 : o0, tile + (4 * g + i) * 512);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = min(rw + 8 * i + (lane >> 3), nrows - 1);
+        dma16(base + (int64_t)r * rs + col(g, lane, i & 1), tile + (4 * g + i) * 512);
+      }
+    }
+  }
+};
+
 // Wave-private row staging -----------------------------------------------------
 //
 // 32 rows x 128 bf16 (8 KB) per wave, 16-byte chunk c of row r at element
