@@ -260,11 +260,16 @@ def _setup_context(ctx, inputs, output):
     q, k, v = inputs
     out, lse = output
     ctx.mark_non_differentiable(lse)
+    # The backward never reads the LSE's gradient: without this autograd fills
+    # a zero tensor for it (one extra kernel launch per backward).
+    ctx.set_materialize_grads(False)
     ctx.save_for_backward(q, k, v, out, lse)
 
 
 def _backward(ctx, dout, dlse):
     q, k, v, out, lse = ctx.saved_tensors
+    if dout is None:  # only possible without materialized grads: no gradient reaches out
+        return None, None, None
     return _fa_bwd(dout, q, k, v, out, lse)
 
 
