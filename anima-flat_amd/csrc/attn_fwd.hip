@@ -80,13 +80,13 @@ struct FwdParams {
   float c;  // softmax_scale * log2(e)
   // Key split of the last work items (see split_plan): blocks past full_blocks
   // each take one of nsplit key ranges of work item full_blocks + j / nsplit
-  // and write normalised fp32 partials (part_o [j][split][256][128],
-  // part_lse [j][split][256]) that attn_fwd_combine_kernel merges.
+  // and write normalised partials (part_o [j][split][256][128] bf16,
+  // part_lse [j][split][256] fp32) that attn_fwd_combine_kernel merges.
   int full_blocks, split_items, nsplit;
   // Workgroups resident at once (one per CU): the unsplit blocks are mapped
   // to work items round by round (see attn_fwd_kernel).
   int round_blocks;
-  float* part_o;
+  bf16* part_o;
   float* part_lse;
 };
 
@@ -338,42 +338,20 @@ struct FwdWave {
     }
   }
 
-  // Partial result of one key range: O / l in fp32 and the range's LSE, for
-  // the combine pass (no padding correction here). `row` is the (item,
-  // split) record; the wave holds queries qloc0 .. qloc0 + 31. Like O in the
-  // epilogue, the fp32 rows go through the wave's 8 KB of LDS, in two halves
-  // of 64 head-dim values (256 B per row), so that each store writes 4 whole
-  // 256-byte half rows.
+  // Partial result of one key range: O / l rounded to bf16 and the range's
+  // LSE (fp32), for the combine pass (no padding correction here). `row` is
+  // the (item, split) record; the wave holds queries qloc0 .. qloc0 + 31. The
+  // rows leave like O in the epilogue (row staging, 4 whole 256-byte rows per
+  // store). In fp32 the partials doubled the bytes a short forward writes and
+  // its combine pass reads (config 1: 33.8 MB).
   __device__ __forceinline__ void store_partial(const FwdParams& p, int64_t row, int qloc0,
                                                 int lane, bf16* stage) const {
     const float l_tot = pair_sum((l4[0] + l4[1]) + (l4[2] + l4[3]));
     const bool any = l_tot > 0.f;
     const float lse = any ? (m_raw * c + __log2f(l_tot)) * kLn2 : -INFINITY;
     const float scale = any ? 1.0f / l_tot : 0.f;
-    float* fst = reinterpret_cast<float*>(stage);
-    float* op = p.part_o + (row * kQPerWg + qloc0) * kD;
-    const int ch = lane & 15;
-#pragma unroll
-    for (int half = 0; half < 2; ++half) {
-#pragma unroll
-      for (int dh = 0; dh < 2; ++dh) {
-        const int dt = 2 * half + dh;
-#pragma unroll
-        for (int rq = 0; rq < 4; ++rq) {
-          // 4 floats at d = 32 dt + 8 rq + 4 hh: 16-byte chunk 8 dh + 2 rq + hh of the half row.
-          const f32x4 v = {o[dt][4 * rq] * scale, o[dt][4 * rq + 1] * scale,
-                           o[dt][4 * rq + 2] * scale, o[dt][4 * rq + 3] * scale};
-          const int c16 = 8 * dh + 2 * rq + hh;
-          *reinterpret_cast<f32x4*>(fst + li * 64 + ((c16 ^ (li & 15)) * 4)) = v;
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int r = (lane >> 4) + 4 * i;
-        const f32x4 v = *reinterpret_cast<const f32x4*>(fst + r * 64 + ((ch ^ (r & 15)) * 4));
-        *reinterpret_cast<f32x4*>(op + r * kD + 64 * half + 4 * ch) = v;
-      }
-    }
+    stage_acc_rows(o, scale, lane, stage);
+    stage_rows_out(p.part_o + row * kQPerWg * kD, kD, qloc0, kQPerWg, lane, stage);
     if (hh == 0) p.part_lse[row * kQPerWg + qloc0 + li] = lse;
   }
 
@@ -539,7 +517,9 @@ __global__ __launch_bounds__(256) void attn_fwd_combine_kernel(FwdParams p) {
     for (int s = 0; s < 8; ++s) {
       if (s < p.nsplit && ls[s] > -INFINITY) {
         const float wgt = expf(ls[s] - lse);
-        acc += wgt * ldf4(p.part_o + ((row0 + s) * kQPerWg + qloc) * kD + d0);
+        const u32x2 raw = *reinterpret_cast<const u32x2*>(p.part_o + ((row0 + s) * kQPerWg + qloc) * kD + d0);
+        const f32x4 v = {bf16_lo(raw[0]), bf16_hi(raw[0]), bf16_lo(raw[1]), bf16_hi(raw[1])};
+        acc += wgt * v;
       }
     }
   }
@@ -582,7 +562,8 @@ static SplitPlan split_plan(int64_t T, int64_t Sk, int ncu) {
 }
 
 static size_t split_workspace_bytes(const SplitPlan& s) {
-  return (size_t)s.split_items * s.nsplit * kQPerWg * (kD + 1) * sizeof(float);
+  // bf16 O rows and one fp32 LSE per query.
+  return (size_t)s.split_items * s.nsplit * kQPerWg * (kD * sizeof(bf16) + sizeof(float));
 }
 
 static int64_t work_items(int64_t B, int64_t Sq, int64_t H) {
@@ -651,18 +632,18 @@ static int prepare(const aa_attn_fwd_args* a, FwdParams& p) {
   p.round_blocks = ncu > 0 ? std::min(ncu, std::max(sp.full_blocks, 1)) : std::max(sp.full_blocks, 1);
   p.split_items = sp.split_items;
   p.nsplit = sp.nsplit;
-  p.part_o = (float*)a->workspace;
-  p.part_lse = p.part_o + (size_t)sp.split_items * sp.nsplit * kQPerWg * kD;
+  p.part_o = (bf16*)a->workspace;
+  p.part_lse = (float*)(p.part_o + (size_t)sp.split_items * sp.nsplit * kQPerWg * kD);
   return AA_OK;
 }
 
 // Split partials of aa_attn_fwd_noalloc. split_plan splits at most ncu / 2
 // items into at most ncu / items key ranges, so the partials never exceed
-// ncu * kQPerWg * (kD + 1) floats (33,816,576 bytes at 256 CUs); the
+// ncu * kQPerWg records of kD bf16 + one float (17,039,360 bytes at 256 CUs); the
 // head-dim-384 forward's never exceed kD384MaxPartialBytes (50,462,720). The
 // array holds the larger, resident on every device the library runs on.
 constexpr size_t kFwdScratchBytes =
-    std::max((size_t)256 * kQPerWg * (kD + 1) * sizeof(float), kD384MaxPartialBytes);
+    std::max((size_t)256 * kQPerWg * (kD * sizeof(bf16) + sizeof(float)), kD384MaxPartialBytes);
 static __device__ __align__(256) uint8_t scratch[kFwdScratchBytes];
 
 // Device address of `scratch` on the current device, looked up once per

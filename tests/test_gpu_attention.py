@@ -134,17 +134,17 @@ def test_large_grid_forward(pkg, B, Sq, Sk, H, lens):
 
 
 def test_forward_workspace(pkg):
-    """A partial last round of work items is split over key ranges (fp32
-    partials in the workspace); a whole number of rounds needs none."""
+    """A partial last round of work items is split over key ranges (bf16
+    partial O and fp32 LSE in the workspace); a whole number of rounds needs none."""
     lib = pkg._lib.lib()
     if torch.cuda.get_device_properties(0).multi_processor_count != 256:
         pytest.skip("sizes below are for 256 CUs (MI355X)")
     assert lib.aa_attn_fwd_workspace(1, 4096, 4096, 16, 128) == 0  # config 2: one full round
     assert lib.aa_attn_fwd_workspace(2, 4096, 4096, 16, 128) == 0  # two full rounds
-    # config 1: 64 items alone on 256 CUs -> 4 key ranges each, 256 x (128 + 1) fp32 per range
-    assert lib.aa_attn_fwd_workspace(1, 1024, 1024, 16, 128) == 64 * 4 * 256 * 129 * 4
+    # config 1: 64 items alone on 256 CUs -> 4 key ranges each, 256 x (128 bf16 + 1 fp32) per range
+    assert lib.aa_attn_fwd_workspace(1, 1024, 1024, 16, 128) == 64 * 4 * 256 * (128 * 2 + 4)
     # config 4b: 576 items = 2 rounds + 64 -> the last 64 split 4 ways
-    assert lib.aa_attn_fwd_workspace(1, 9216, 9216, 16, 128) == 64 * 4 * 256 * 129 * 4
+    assert lib.aa_attn_fwd_workspace(1, 9216, 9216, 16, 128) == 64 * 4 * 256 * (128 * 2 + 4)
 
 
 @pytest.mark.parametrize("lens", [[37, 80], [1, 64], [80, 80], [65, 3]])
