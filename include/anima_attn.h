@@ -196,10 +196,11 @@ typedef struct aa_attn_fwd_args {
   size_t workspace_bytes;
 } aa_attn_fwd_args;
 
-/* Bytes of device workspace aa_attn_fwd needs on the current device: fp32
- * partial results when the work items (256 queries of one (batch, head); 128
- * at hd 384) of a partial last round of workgroups (at hd 384: of too few
- * work items to fill the device) are split over key ranges, else 0. */
+/* Bytes of device workspace aa_attn_fwd needs on the current device: partial
+ * results (hd 128: bf16 O and fp32 LSE; hd 384: fp32) when the work items (256
+ * queries of one (batch, head); 128 at hd 384) of a partial last round of
+ * workgroups (at hd 384: of too few work items to fill the device) are split
+ * over key ranges, else 0. */
 size_t aa_attn_fwd_workspace(int64_t B, int64_t Sq, int64_t Sk, int64_t H, int64_t hd);
 
 /*
