@@ -640,7 +640,7 @@ static int prepare(const aa_attn_fwd_args* a, FwdParams& p) {
 // Split partials of aa_attn_fwd_noalloc. split_plan splits at most ncu / 2
 // items into at most ncu / items key ranges, so the partials never exceed
 // ncu * kQPerWg records of kD bf16 + one float (17,039,360 bytes at 256 CUs); the
-// head-dim-384 forward's never exceed kD384MaxPartialBytes (50,462,720). The
+// head-dim-384 forward's never exceed kD384MaxPartialBytes (25,296,896). The
 // array holds the larger, resident on every device the library runs on.
 constexpr size_t kFwdScratchBytes =
     std::max((size_t)256 * kQPerWg * (kD * sizeof(bf16) + sizeof(float)), kD384MaxPartialBytes);

@@ -7,8 +7,8 @@
 namespace aa {
 
 // Most bytes of split partials the d=384 forward needs on a 256-CU device
-// (256 key ranges x 128 queries x (384 + 1) floats).
-constexpr size_t kD384MaxPartialBytes = (size_t)256 * 128 * 385 * sizeof(float);
+// (256 key ranges x 128 queries x (384 bf16 + 1 float)).
+constexpr size_t kD384MaxPartialBytes = (size_t)256 * 128 * (384 * 2 + 4);
 
 // Bytes of split partials the d=384 forward needs on a device with ncu CUs.
 size_t attn_fwd_d384_workspace(int64_t B, int64_t Sq, int64_t Sk, int64_t H, int ncu);

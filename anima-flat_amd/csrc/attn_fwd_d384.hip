@@ -76,7 +76,7 @@ struct Params {
   int64_t os0, os1, os2;
   int H, Sq, Sk, nqblk, items, nsplit;
   float c;  // softmax_scale * log2(e)
-  float* part_o;    // [items * nsplit][128][384] normalised fp32 partials
+  bf16* part_o;     // [items * nsplit][128][384] normalised partials, bf16
   float* part_lse;  // [items * nsplit][128]
 };
 
@@ -463,32 +463,29 @@ void attn_fwd_d384_kernel(Params p) {
   const bool any = l_tot > 0.f;
   const float lse = any ? (w.m_raw * w.c + __log2f(l_tot)) * kLn2 : -INFINITY;
   float scale = any ? 1.0f / l_tot : 0.f;
-  if (p.nsplit == 1) {
-    if (p.ln_pad) scale *= 1.0f / (1.0f + expf(p.ln_pad[it.b] - lse));
-    __syncthreads();  // every wave is done with the ring
-    bf16* st = lds + wave * 4096;
-    bf16* obase = p.o + it.b * p.os0 + it.h * p.os2;
+  // O rows (or the range's partial O, normalised like O and rounded to bf16,
+  // with its LSE in fp32) leave through LDS row staging, 4 whole 256-byte rows
+  // per store.
+  const bool partial = p.nsplit > 1;
+  const int64_t rec = (int64_t)item * p.nsplit + split;
+  if (!partial && p.ln_pad) scale *= 1.0f / (1.0f + expf(p.ln_pad[it.b] - lse));
+  __syncthreads();  // every wave is done with the ring
+  bf16* st = lds + wave * 4096;
+  bf16* obase = partial ? p.part_o + rec * kQPerWg * kD : p.o + it.b * p.os0 + it.h * p.os2;
+  const int64_t ors = partial ? (int64_t)kD : p.os1;
+  const int orow0 = partial ? wave * 32 : qrow0;
+  const int onrows = partial ? kQPerWg : p.Sq;
 #pragma unroll
-    for (int j = 0; j < kChunks; ++j) {
-      const f32x16 oj[4] = {w.o[4 * j], w.o[4 * j + 1], w.o[4 * j + 2], w.o[4 * j + 3]};
-      stage_acc_rows(oj, scale, lane, st);
-      stage_rows_out(obase + 128 * j, p.os1, qrow0, p.Sq, lane, st);
-    }
+  for (int j = 0; j < kChunks; ++j) {
+    const f32x16 oj[4] = {w.o[4 * j], w.o[4 * j + 1], w.o[4 * j + 2], w.o[4 * j + 3]};
+    stage_acc_rows(oj, scale, lane, st);
+    stage_rows_out(obase + 128 * j, ors, orow0, onrows, lane, st);
+  }
+  if (partial) {
+    if (w.hh == 0) p.part_lse[rec * kQPerWg + wave * 32 + w.li] = lse;
+  } else {
     const int qrow = qrow0 + w.li;
     if (p.lse && w.hh == 0 && qrow < p.Sq) p.lse[((int64_t)it.b * p.H + it.h) * p.Sq + qrow] = lse;
-  } else {
-    const int64_t rec = (int64_t)item * p.nsplit + split;
-    const int qloc = wave * 32 + w.li;
-    float* op = p.part_o + (rec * kQPerWg + qloc) * kD + 4 * w.hh;
-#pragma unroll
-    for (int db = 0; db < 12; ++db)
-#pragma unroll
-      for (int rq = 0; rq < 4; ++rq) {
-        const f32x4 v = {w.o[db][4 * rq] * scale, w.o[db][4 * rq + 1] * scale,
-                         w.o[db][4 * rq + 2] * scale, w.o[db][4 * rq + 3] * scale};
-        *reinterpret_cast<f32x4*>(op + 32 * db + 8 * rq) = v;
-      }
-    if (w.hh == 0) p.part_lse[rec * kQPerWg + qloc] = lse;
   }
 }
 
@@ -521,7 +518,11 @@ __global__ __launch_bounds__(192) void attn_fwd_d384_combine_kernel(Params p) {
 #pragma unroll
     for (int s = 0; s < kMaxSplit; ++s)
       if (s < p.nsplit && ls[s] > -INFINITY)
-        acc += expf(ls[s] - lse) * ldf4(p.part_o + ((rec0 + s) * kQPerWg + qloc) * kD + d0);
+      {
+        const u32x2 raw = *reinterpret_cast<const u32x2*>(p.part_o + ((rec0 + s) * kQPerWg + qloc) * kD + d0);
+        const f32x4 v = {bf16_lo(raw[0]), bf16_hi(raw[0]), bf16_lo(raw[1]), bf16_hi(raw[1])};
+        acc += expf(ls[s] - lse) * v;
+      }
   }
   float scale = 1.f;
   if (p.ln_pad) scale = 1.0f / (1.0f + expf(p.ln_pad[it.b] - lse));
@@ -549,7 +550,7 @@ static int64_t items_of(int64_t B, int64_t Sq, int64_t H) {
 
 static size_t partial_bytes(int64_t items, int nsplit) {
   if (nsplit <= 1) return 0;
-  return (size_t)items * nsplit * kQPerWg * (kD + 1) * sizeof(float);
+  return (size_t)items * nsplit * kQPerWg * (kD * sizeof(bf16) + sizeof(float));  // bf16 O, fp32 LSE
 }
 
 }  // namespace d384
@@ -606,8 +607,8 @@ int attn_fwd_d384(const aa_attn_fwd_args* a, int ncu, hipStream_t stream) {
   p.items = (int)items;
   p.nsplit = nsplit;
   p.c = a->softmax_scale * kLog2e;
-  p.part_o = need > 0 ? (float*)a->workspace : nullptr;
-  p.part_lse = need > 0 ? p.part_o + (size_t)items * nsplit * kQPerWg * kD : nullptr;
+  p.part_o = need > 0 ? (bf16*)a->workspace : nullptr;
+  p.part_lse = need > 0 ? (float*)(p.part_o + (size_t)items * nsplit * kQPerWg * kD) : nullptr;
 
   attn_fwd_d384_kernel<<<dim3((unsigned)(items * nsplit)), kWaves * 64, 0, stream>>>(p);
   if (int rc = check_launch("attn_fwd d384")) return rc;

@@ -221,7 +221,7 @@ int aa_attn_fwd(const aa_attn_fwd_args* args, void* stream);
 
 /*
  * aa_attn_fwd without a caller workspace and without any allocation: the
- * split partials go to a fixed device array of 50,462,720 bytes that the
+ * split partials go to a fixed device array of 25,296,896 bytes that the
  * library holds on each device it runs on until the process ends (every
  * forward, head_dim 128 or 384, on a 256-CU device fits; a plan that needs
  * more returns AA_EUNSUPPORTED). args->workspace / workspace_bytes are ignored. Calls on
