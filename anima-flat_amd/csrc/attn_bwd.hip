@@ -6,9 +6,15 @@
 //   dV = P^T dO, dP = dO V^T, dZ = P o (dP - D) with D = rowsum(dO o O),
 //   dK = scale * dZ^T Q, dQ = scale * dZ K.
 //
-// Three kernels:
-// 1. prep_kernel, one workgroup per (64-query tile, head, batch): writes a
-//    1 KB record of lse * log2(e) and -D per 64 queries.
+// Two kernels, launched in this order:
+// 1. dq_kernel: 8 waves x 32 queries per workgroup, two groups one phase
+//    apart; streams 64-key tiles (K rows, V rows: 32 KB) and reads K^T from
+//    the K rows with transposed LDS reads (dQ leaves through LDS row
+//    staging). Queries are the columns:
+//      S^T = K Q^T, dP^T = V dO^T, dQ^T += K^T dZ^T.
+//    Each query's lse * log2(e) and -D (D = rowsum(dO o O), from the dO^T
+//    operands it holds and one read of O) it computes itself and writes to a
+//    1 KB stats record per 64 queries for the second kernel.
 // 2. dkdv_kernel: 8 waves, 128 keys per workgroup (32 per wave pair, split
 //    by role, the roles one phase apart, at the kernel); streams 64-query
 //    tiles (Q rows, dO rows, stats: 33 KB) into LDS by DMA and reads Q^T and
@@ -19,11 +25,6 @@
 //      dP = dO V^T       A = dO rows (LDS), B = V^T (registers)
 //      dV^T += dO^T P    A = dO^T (LDS),    B = P from the S accumulators
 //      dK^T += Q^T dZ    A = Q^T (LDS),     B = dZ from the accumulators
-// 3. dq_kernel: 8 waves x 32 queries per workgroup, two groups one phase
-//    apart; streams 64-key tiles (K rows, V rows: 32 KB) and reads K^T from
-//    the K rows with transposed LDS reads (dQ leaves through LDS row
-//    staging). Queries are the columns:
-//      S^T = K Q^T, dP^T = V dO^T, dQ^T += K^T dZ^T.
 // The transposed reads list the keys / queries of each 16-column chunk in the
 // accumulator row order, so the bf16-rounded accumulators are the B operands
 // as they are.
@@ -55,39 +56,6 @@ struct Params {
   float c;      // scale * log2(e)
   float scale;  // softmax scale
 };
-
-// ---------------------------------------------------------------- prep --
-
-__global__ __launch_bounds__(256) void prep_kernel(Params p) {
-  const int t = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-  const int64_t bh = (int64_t)b * p.H + h;
-  const int tid = threadIdx.x;
-  const int q0 = t * kT;
-  // D = rowsum(dO * O): 4 lanes per row, 32 values each. Rows past Sq get
-  // lse2 = +inf (P = 0) and D = 0.
-  const int row = tid >> 2, part = tid & 3;
-  const int q = q0 + row;
-  float d = 0.f;
-  if (q < p.Sq) {
-    const bf16* dop = p.dout + b * p.s_do[0] + (int64_t)q * p.s_do[1] + h * p.s_do[2] + 32 * part;
-    const bf16* op = p.o + b * p.s_o[0] + (int64_t)q * p.s_o[1] + h * p.s_o[2] + 32 * part;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float x[8], y[8];
-      unpack8(ld16(dop + 8 * j), x);
-      unpack8(ld16(op + 8 * j), y);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) d = fmaf(x[i], y[i], d);
-    }
-  }
-  d = group_sum<4>(d);
-  float* st = p.stats + (bh * p.ntq + t) * kStat;
-  if (part == 0) {
-    st[row] = q < p.Sq ? p.lse[bh * p.Sq + q] * kLog2e : INFINITY;
-    st[kT + row] = -d;
-  }
-  if (tid < kStat - 2 * kT) st[2 * kT + tid] = 0.f;
-}
 
 // ------------------------------------------------------------ dK, dV --
 
@@ -364,11 +332,32 @@ void dq_kernel(Params p, int nqblk, int total_blocks) {
       doreg[kk] = as_bf16x8(e);
     }
   }
+  // The query's stats: lse2 = lse * log2(e) and -D, D = rowsum(dO o O) (this
+  // lane's 64 values against its dO^T operands, then the partner lane's
+  // half). They also go to the query's stats record, which dkdv_kernel reads
+  // (it runs after this kernel): rows past Sq get lse2 = +inf (P = 0) and
+  // D = 0, and every record's second half is the zero pad dkdv uses to start
+  // its S accumulators.
   float lse2 = INFINITY, ndlt = 0.f;  // -D
   if (q_ok) {
-    const float* st = p.stats + ((int64_t)bh * p.ntq + qrow / kT) * kStat + (qrow % kT);
-    lse2 = st[0];
-    ndlt = st[kT];
+    lse2 = p.lse[(int64_t)bh * p.Sq + qrow] * kLog2e;
+    const bf16* op = p.o + b * p.s_o[0] + h * p.s_o[2] + (int64_t)qrow * p.s_o[1] + 8 * hh;
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+      float x[8], y[8];
+      unpack8(ld16(op + 16 * kk), x);
+      unpack8(__builtin_bit_cast(u32x4, doreg[kk]), y);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ndlt = fmaf(y[i], x[i], ndlt);
+    }
+  }
+  ndlt = -pair_sum(ndlt);
+  if (hh == 0 && qrow < p.ntq * kT) {
+    float* st = p.stats + ((int64_t)bh * p.ntq + qrow / kT) * kStat + (qrow % kT);
+    st[0] = lse2;
+    st[kT] = ndlt;
+    st[2 * kT] = 0.f;
+    st[3 * kT] = 0.f;
   }
 
   const bf16* kbase = p.k + b * p.s_k[0] + h * p.s_k[2];
@@ -619,22 +608,19 @@ extern "C" int aa_attn_bwd(const aa_attn_bwd_args* a, void* workspace, size_t wo
   hipStream_t st = (hipStream_t)stream;
 
   const int64_t BH = a->B * a->H;
+  // dq_kernel first: it writes the stats records that dkdv_kernel reads.
   // Nothing reads the workspace when Sq == 0 (dK = dV = 0 and no dQ rows).
   if (a->Sq > 0) {
-    bwd::prep_kernel<<<dim3((unsigned)p.ntq, (unsigned)a->H, (unsigned)a->B), 256, 0, st>>>(p);
-    if (int rc = check_launch("attn_bwd prep")) return rc;
+    const int nqblk = (int)((a->Sq + bwd::kQueriesPerWg - 1) / bwd::kQueriesPerWg);
+    const int total = (int)(BH * nqblk);
+    bwd::dq_kernel<<<dim3((unsigned)total), bwd::kDqWaves * 64, 0, st>>>(p, nqblk, total);
+    if (int rc = check_launch("attn_bwd dq")) return rc;
   }
   if (a->Sk > 0) {
     const int nkblk = (int)((a->Sk + bwd::kKeysPerWg - 1) / bwd::kKeysPerWg);
     const int total = (int)(BH * nkblk);
     bwd::dkdv_kernel<<<dim3((unsigned)total), bwd::kDkWaves * 64, 0, st>>>(p, nkblk, total);
     if (int rc = check_launch("attn_bwd dkdv")) return rc;
-  }
-  if (a->Sq > 0) {
-    const int nqblk = (int)((a->Sq + bwd::kQueriesPerWg - 1) / bwd::kQueriesPerWg);
-    const int total = (int)(BH * nqblk);
-    bwd::dq_kernel<<<dim3((unsigned)total), bwd::kDqWaves * 64, 0, st>>>(p, nqblk, total);
-    if (int rc = check_launch("attn_bwd dq")) return rc;
   }
   return AA_OK;
 }
