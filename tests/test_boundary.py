@@ -88,9 +88,7 @@ def test_workspace_sizes(lib):
     # one 1 KB stats record per 64-query tile, per (batch, head)
     assert lib.aa_attn_bwd_workspace(2, 100, 77, 3, 128) == 2 * 3 * 2 * 1024
     assert lib.aa_attn_bwd_workspace(1, 0, 77, 3, 128) == 0
-    # weight-gradient partials: one [2][128] (or [128]) fp32 record per 8 tokens,
-    # then one per 16 records (the two-level reduction).
-    # One record of weight-gradient partial sums per 8 tokens.
+    # weight-gradient partials: one [2][128] (or [128]) fp32 record per 8 tokens
     assert lib.aa_qkv_norm_rope_bwd_workspace(1, 4096, 16, 128) == 512 * 2 * 128 * 4
     assert lib.aa_head_norm_bwd_workspace(2, 9, 5, 128) == 3 * 128 * 4
     # one int32 per 32 context rows per item
@@ -307,3 +305,33 @@ def test_bench_rejects_more_than_one_gpu():
 
 def test_package_loads_once():
     assert __graft_entry__.load_package() is __graft_entry__.load_package()
+
+
+def test_negative_or_huge_sequence_strides_are_rejected(pkg, lib):
+    """The tile DMA addresses K/V (forward) and Q/dO/K/V (backward) rows by a
+    32-bit unsigned per-lane offset from a scalar row base, so a negative or
+    >= 2^24 token stride must fail validation, before anything touches the device
+    (the pointers below are never dereferenced)."""
+    L = pkg._lib
+    fake = 1 << 20  # 16-byte aligned, never read
+    base = (1 << 15, 2048, 128)  # [B, S, H, 128] strides, elements
+    a = L.AttnFwdArgs()
+    a.q = a.k = a.v = a.out = fake
+    a.B, a.Sq, a.Sk, a.H, a.hd, a.dtype, a.softmax_scale = 1, 64, 64, 16, 128, 0, 0.088
+    for name in ("q_stride", "k_stride", "v_stride", "out_stride"):
+        setattr(a, name, L.c_strides(base))
+    for bad in (-2048, 1 << 24):
+        a.k_stride = L.c_strides((1 << 15, bad, 128))
+        assert lib.aa_attn_fwd(ctypes.byref(a), None) == L.AA_EUNSUPPORTED
+        assert "sequence stride" in lib.aa_last_error().decode()
+    b = L.AttnBwdArgs()
+    b.dout = b.q = b.k = b.v = b.out = b.lse = b.dq = b.dk = b.dv = fake
+    b.B, b.Sq, b.Sk, b.H, b.hd, b.dtype, b.softmax_scale = 1, 64, 64, 16, 128, 0, 0.088
+    for name in ("dout_stride", "q_stride", "k_stride", "v_stride", "out_stride", "dq_stride",
+                 "dk_stride", "dv_stride"):
+        setattr(b, name, L.c_strides(base))
+    for name in ("dout_stride", "q_stride", "k_stride", "v_stride"):
+        setattr(b, name, L.c_strides((1 << 15, -2048, 128)))
+        assert lib.aa_attn_bwd(ctypes.byref(b), None, 0, None) == L.AA_EUNSUPPORTED, name
+        assert "sequence stride" in lib.aa_last_error().decode()
+        setattr(b, name, L.c_strides(base))
