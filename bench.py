@@ -298,7 +298,8 @@ def main() -> int:
     if args.gpus != 1:
         print(
             f"bench.py: --gpus {args.gpus} is not supported: this build measures one GPU "
-            "(the path shards over batch and heads with no exchange; see DESIGN.md)",
+            "(the path shards over batch and heads with no exchange between GPUs: each GPU runs "
+            "these kernels on its share)",
             file=sys.stderr,
         )
         return 2
