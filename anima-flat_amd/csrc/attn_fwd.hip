@@ -486,18 +486,20 @@ void attn_fwd_kernel(FwdParams p) {
   else w.store_partial(p, (int64_t)(item_idx - p.full_blocks) * p.nsplit + split, wave * 32, lane, stage);
 }
 
-// Merges the key-range partials of the split work items: 8 queries per
-// workgroup, 32 lanes per query with 4 head-dim values each. O = sum_s
-// exp(lse_s - lse) O_s with lse = log sum_s exp(lse_s), then the optional
-// padding correction, bf16 O and LSE.
+// Merges the key-range partials of the split work items: 16 queries per
+// workgroup, 16 lanes per query with 8 head-dim values (16 bytes) each.
+// O = sum_s exp(lse_s - lse) O_s with lse = log sum_s exp(lse_s), then the
+// optional padding correction, bf16 O and LSE. (With 4 values per lane the
+// pass ran at ~2.6 TB/s: too few bytes in flight per lane.)
+constexpr int kCombineQ = 16;  // queries per combine workgroup
 __global__ __launch_bounds__(256) void attn_fwd_combine_kernel(FwdParams p) {
-  const int gq = blockIdx.x * 8 + (threadIdx.x >> 5);  // split-item query index
+  const int gq = blockIdx.x * kCombineQ + (threadIdx.x >> 4);  // split-item query index
   const int j = gq / kQPerWg, qloc = gq - j * kQPerWg;
   if (j >= p.split_items) return;
   const Item it = decode_item(p, p.full_blocks + j);
   const int qrow = it.qblk * kQPerWg + qloc;
   if (qrow >= p.Sq) return;
-  const int d0 = 4 * (threadIdx.x & 31);
+  const int d0 = 8 * (threadIdx.x & 15);
   const int64_t row0 = (int64_t)j * p.nsplit;
   float ls[8];
   float mx = -INFINITY;
@@ -507,7 +509,7 @@ __global__ __launch_bounds__(256) void attn_fwd_combine_kernel(FwdParams p) {
     mx = fmaxf(mx, ls[s]);
   }
   float lse = -INFINITY;
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   if (mx > -INFINITY) {
     float sum = 0.f;
 #pragma unroll
@@ -517,17 +519,19 @@ __global__ __launch_bounds__(256) void attn_fwd_combine_kernel(FwdParams p) {
     for (int s = 0; s < 8; ++s) {
       if (s < p.nsplit && ls[s] > -INFINITY) {
         const float wgt = expf(ls[s] - lse);
-        const u32x2 raw = *reinterpret_cast<const u32x2*>(p.part_o + ((row0 + s) * kQPerWg + qloc) * kD + d0);
-        const f32x4 v = {bf16_lo(raw[0]), bf16_hi(raw[0]), bf16_lo(raw[1]), bf16_hi(raw[1])};
-        acc += wgt * v;
+        float v[8];
+        unpack8(ld16(p.part_o + ((row0 + s) * kQPerWg + qloc) * kD + d0), v);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] = fmaf(wgt, v[i], acc[i]);
       }
     }
   }
   float scale = 1.f;
   if (p.ln_pad) scale = 1.0f / (1.0f + expf(p.ln_pad[it.b] - lse));
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] *= scale;
   bf16* op = p.o + it.b * p.os0 + (int64_t)qrow * p.os1 + it.h * p.os2 + d0;
-  const u32x2 w = {pack_bf16(acc[0] * scale, acc[1] * scale), pack_bf16(acc[2] * scale, acc[3] * scale)};
-  *reinterpret_cast<u32x2*>(op) = w;
+  st16_nt(op, pack8(acc));
   if (p.lse && d0 == 0) p.lse[((int64_t)it.b * p.H + it.h) * p.Sq + qrow] = lse;
 }
 
@@ -708,7 +712,7 @@ extern "C" int aa_attn_fwd(const aa_attn_fwd_args* a, void* stream) {
   attn_fwd_kernel<<<dim3((unsigned)blocks), kWaves * 64, 0, st>>>(p);
   if (int rc = check_launch("attn_fwd")) return rc;
   if (p.split_items > 0) {
-    const int groups = (p.split_items * kQPerWg + 7) / 8;
+    const int groups = (p.split_items * kQPerWg + kCombineQ - 1) / kCombineQ;
     attn_fwd_combine_kernel<<<dim3((unsigned)groups), 256, 0, st>>>(p);
     return check_launch("attn_fwd combine");
   }

@@ -489,17 +489,18 @@ void attn_fwd_d384_kernel(Params p) {
   }
 }
 
-// Merges the key-range partials: 2 queries per workgroup, 96 lanes per query
-// with 4 head-dim values each. O = sum_s exp(lse_s - lse) O_s with
+// Merges the key-range partials: 4 queries per workgroup, 48 lanes per query
+// with 8 head-dim values (16 bytes) each. O = sum_s exp(lse_s - lse) O_s with
 // lse = log sum_s exp(lse_s), then the optional padding correction.
+constexpr int kCombineQ = 4;  // queries per combine workgroup
 __global__ __launch_bounds__(192) void attn_fwd_d384_combine_kernel(Params p) {
-  const int gq = blockIdx.x * 2 + (int)threadIdx.x / 96;  // item * 128 + local query
+  const int gq = blockIdx.x * kCombineQ + (int)threadIdx.x / 48;  // item * 128 + local query
   const int item = gq / kQPerWg, qloc = gq - item * kQPerWg;
   if (item >= p.items) return;
   const Item it = decode_item(p, item);
   const int qrow = it.qblk * kQPerWg + qloc;
   if (qrow >= p.Sq) return;
-  const int d0 = 4 * ((int)threadIdx.x % 96);
+  const int d0 = 8 * ((int)threadIdx.x % 48);
   const int64_t rec0 = (int64_t)item * p.nsplit;
   float ls[kMaxSplit];
   float mx = -INFINITY;
@@ -509,7 +510,7 @@ __global__ __launch_bounds__(192) void attn_fwd_d384_combine_kernel(Params p) {
     mx = fmaxf(mx, ls[s]);
   }
   float lse = -INFINITY;
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   if (mx > -INFINITY) {
     float sum = 0.f;
 #pragma unroll
@@ -517,18 +518,20 @@ __global__ __launch_bounds__(192) void attn_fwd_d384_combine_kernel(Params p) {
     lse = mx + logf(sum);
 #pragma unroll
     for (int s = 0; s < kMaxSplit; ++s)
-      if (s < p.nsplit && ls[s] > -INFINITY)
-      {
-        const u32x2 raw = *reinterpret_cast<const u32x2*>(p.part_o + ((rec0 + s) * kQPerWg + qloc) * kD + d0);
-        const f32x4 v = {bf16_lo(raw[0]), bf16_hi(raw[0]), bf16_lo(raw[1]), bf16_hi(raw[1])};
-        acc += expf(ls[s] - lse) * v;
+      if (s < p.nsplit && ls[s] > -INFINITY) {
+        const float wgt = expf(ls[s] - lse);
+        float v[8];
+        unpack8(ld16(p.part_o + ((rec0 + s) * kQPerWg + qloc) * kD + d0), v);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] = fmaf(wgt, v[i], acc[i]);
       }
   }
   float scale = 1.f;
   if (p.ln_pad) scale = 1.0f / (1.0f + expf(p.ln_pad[it.b] - lse));
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] *= scale;
   bf16* op = p.o + it.b * p.os0 + (int64_t)qrow * p.os1 + it.h * p.os2 + d0;
-  const u32x2 wv = {pack_bf16(acc[0] * scale, acc[1] * scale), pack_bf16(acc[2] * scale, acc[3] * scale)};
-  *reinterpret_cast<u32x2*>(op) = wv;
+  st16_nt(op, pack8(acc));
   if (p.lse && d0 == 0) p.lse[((int64_t)it.b * p.H + it.h) * p.Sq + qrow] = lse;
 }
 
@@ -613,7 +616,7 @@ int attn_fwd_d384(const aa_attn_fwd_args* a, int ncu, hipStream_t stream) {
   attn_fwd_d384_kernel<<<dim3((unsigned)(items * nsplit)), kWaves * 64, 0, stream>>>(p);
   if (int rc = check_launch("attn_fwd d384")) return rc;
   if (nsplit > 1) {
-    attn_fwd_d384_combine_kernel<<<dim3((unsigned)(items * kQPerWg / 2)), 192, 0, stream>>>(p);
+    attn_fwd_d384_combine_kernel<<<dim3((unsigned)(items * kQPerWg / kCombineQ)), 192, 0, stream>>>(p);
     return check_launch("attn_fwd d384 combine");
   }
   return AA_OK;
