@@ -15,8 +15,10 @@ Opt-in modules, not imported here (import them explicitly):
                     quantisation of the attention output). The reference's fp8.py registers the
                     same op name and holds the rest of the FP8 path, so importing this module by
                     default would clash with it.
-  kernels.proj   fused QKV projection + prologue (qkv_proj_norm_rope, op
-                 anima_flat_amd::qkv_proj_norm_rope); no counterpart in the reference.
+  kernels.proj   input projections with their normalisation fused (qkv_proj_norm_rope,
+                 proj_head_norm, kv_proj_norm; ops anima_flat_amd::qkv_proj_norm_rope /
+                 proj_head_norm / kv_proj_norm): the GEMM + norm pairs of src/model.py:308-316,
+                 :324 and :256-258 in one kernel each; no single counterpart in the reference.
 
 Every op is registered through kernels.common.custom_op, which raises if the name is already
 registered in the process (torch.library would otherwise re-bind it silently). Ops this package
