@@ -15,7 +15,8 @@
 // Main loop: waves of 64 tokens x WN columns (2 x WN/32 accumulators), over K
 // in stages of 64: the stage's X and W rows move L2 -> LDS by DMA
 // (global_load_lds_dwordx4, no registers) into a ring of two stages, one
-// ahead, one barrier per stage. Each DMA instruction moves 8 rows x 128 bytes,
+// ahead (each wave's share issued over the first k-steps of the stage before),
+// one barrier per stage. Each DMA instruction moves 8 rows x 128 bytes,
 // whole cache lines: with 16 rows x 64 bytes (half lines) per instruction the
 // same loads stream at well under half the rate, which bounded this kernel.
 // A stage in LDS is blocks of 8 rows x 64 k (1 KiB, one DMA instruction);
@@ -65,6 +66,14 @@ struct ProjTile {
   static constexpr int kBPW = kBlocks / kWaves;        // ... per wave
   static constexpr int kCB = WN / 32;                  // 32-column blocks per wave
   static constexpr int kRingElems = 2 * kStageElems;
+  // The next stage's DMA of a wave goes out in this many parts, one per
+  // k-step from the first: the load path takes one instruction per ~11
+  // cycles, so 8 waves issuing 8-10 each at once hold most of them back from
+  // their MFMAs for up to ~900 cycles. Two parts: QKV B=1 99.6 -> 95.5 us
+  // (tile B), xq 64.7 -> 62.2 us (tile A); four parts were slower, and so was
+  // splitting at all with four waves (tile C, whose two workgroups per CU
+  // already overlap one's loads with the other's MFMAs).
+  static constexpr int kDmaParts = kWaves == 8 ? 2 : 1;
   // Sections staged per epilogue pass (the ring holds the staged bf16 tiles).
   static constexpr int kPassSecs = PS;
   static_assert(MT % 64 == 0 && kN % WN == 0 && WN % 32 == 0, "wave tiling");
@@ -139,12 +148,14 @@ __global__ __launch_bounds__(T::kThreads) void qkv_proj_kernel(ProjParams p) {
   // contiguous (block b at b * 512); wave w moves blocks w G .. w G + G - 1.
   // A last stage of 32 k (K % 64 == 32) loads chunks 4..7 from chunks 0..3
   // (in bounds; those products are not computed).
-  auto issue = [&](int s) {
+  // Blocks lo .. hi - 1 of the wave's share of stage s.
+  auto issue = [&](int s, int lo, int hi) {
     bf16* st = lds + (s & 1) * T::kStageElems;
     const int k0 = s * kPK;
     const int cmask = p.K - k0 >= kPK ? 7 : 3;
 #pragma unroll
     for (int i = 0; i < T::kBPW; ++i) {
+      if (i < lo || i >= hi) continue;
       // Wave-uniform: block b, its first row b0 (clamped), the source matrix.
       const int b = wave * T::kBPW + i;
       const bool is_x = b < T::kMT / 8;
@@ -160,7 +171,7 @@ __global__ __launch_bounds__(T::kThreads) void qkv_proj_kernel(ProjParams p) {
 
   const int nk = (p.K + kPK - 1) / kPK;
   const int nfull = p.K / kPK;  // stages of 64 k; a last one of 32 when K % 64 == 32
-  issue(0);
+  issue(0, 0, T::kBPW);
 
   constexpr int kWavesM = T::kMT / 64;
   const int wm = wave % kWavesM;  // tokens 64 wm .. 64 wm + 63
@@ -181,10 +192,10 @@ __global__ __launch_bounds__(T::kThreads) void qkv_proj_kernel(ProjParams p) {
       for (int e = 0; e < 16; ++e) acc[c][t][e] = 0.f;
 
   // One stage of NSTEPS k-steps. Operands of kPre k-steps are read ahead of
-  // their MFMAs: those of the first kPre steps before the next DMA goes out
-  // (its asm is a compiler memory barrier, so they cannot sink to their
-  // MFMAs, and its issue time does not delay the stage's first MFMA), the
-  // rest kPre steps ahead. With 192 accumulator registers (kCB = 6) only one
+  // their MFMAs: those of the first kPre steps before the next stage's DMA
+  // starts going out (its asm is a compiler memory barrier, so they cannot
+  // sink to their MFMAs), the rest kPre steps ahead. The DMA goes out in
+  // kDmaParts parts, one at the start of each of the first k-steps. With 192 accumulator registers (kCB = 6) only one
   // k-step's operands fit beside them at two waves per SIMD.
   constexpr int kPre = T::kCB <= 4 ? 2 : 1;
   auto stage = [&](int s, auto nsteps) {
@@ -207,9 +218,14 @@ __global__ __launch_bounds__(T::kThreads) void qkv_proj_kernel(ProjParams p) {
     };
 #pragma unroll
     for (int kk = 0; kk < kPre && kk < NSTEPS; ++kk) read(kk);
-    if (s + 1 < nk) issue(s + 1);
+    constexpr int kParts = T::kDmaParts < NSTEPS ? T::kDmaParts : NSTEPS;
+    auto part = [&](int j) {
+      if (s + 1 < nk) issue(s + 1, j * T::kBPW / kParts, (j + 1) * T::kBPW / kParts);
+    };
+    part(0);
 #pragma unroll
     for (int kk = 0; kk < NSTEPS; ++kk) {
+      if (kk >= 1 && kk < kParts) part(kk);
       if constexpr (kPre > 1) {
         if (kk + kPre < NSTEPS) read(kk + kPre);
       }
@@ -303,8 +319,8 @@ enum SegMode { kCopy = 0, kNorm = 1, kNormRope = 2 };
 // Tile shape for ntok tokens x nsec sections: 0 = TileA, 1 = TileB, 2 =
 // TileC, the one with the least time on the busiest CU: whole rounds of
 // workgroups over the chip (TileC runs two per CU) times the time of one
-// round. Round times measured on MI355X at K = 2048 (graph-timed): A 62 us,
-// B 99 us, C 36.5 us (two workgroups) -> weights 2.0, 3.2, 2 x 0.59. Ties go
+// round. Round times measured on MI355X at K = 2048 (graph-timed): A 60 us,
+// B 95 us, C 36.5 us (two workgroups) -> weights 1.93, 3.07, 2 x 0.59. Ties go
 // to the lower index. The environment variable AA_PROJ_TILE = a, b or c
 // forces a shape (all give identical results); any other value is an error
 // (-1).
@@ -317,8 +333,8 @@ static int pick_tile(int64_t ntok, int64_t nsec) {
   struct Shape {
     int64_t mt, ns, per_cu;
     double weight;  // time of one round, per workgroup on a CU
-  } shapes[3] = {{TileA::kMT, TileA::kNS, 1, 2.0},
-                 {TileB::kMT, TileB::kNS, 1, 3.2},
+  } shapes[3] = {{TileA::kMT, TileA::kNS, 1, 1.93},
+                 {TileB::kMT, TileB::kNS, 1, 3.07},
                  {TileC::kMT, TileC::kNS, 2, 0.59}};
   int best = 0;
   double best_cost = 0;
