@@ -477,7 +477,19 @@ def main() -> int:
                 "linear_plus_prologue_us": round(us_sp * 1e3, 2),
                 "what": "qkv_proj_norm_rope vs F.linear (hipBLASLt) + qkv_norm_rope, B=1, 4096 tokens",
             }
-            del hid, wq
+            # The same at B=2 (the two CFG branches of a denoiser step in one batch).
+            hid2 = torch.randn(2, S, H * d, device=dev, dtype=BF)
+            proj_fused2 = lambda: proj.qkv_proj_norm_rope(hid2, wq, p["q_weight"], p["k_weight"], p["cos"], p["sin"], H, eps)
+            proj_split2 = lambda: pkg.qkv_norm_rope(torch.nn.functional.linear(hid2, wq), p["q_weight"],
+                                                    p["k_weight"], p["cos"], p["sin"], H, eps)
+            us_fu2, us_sp2 = time_graph(proj_fused2), time_graph(proj_split2)
+            extras["qkv_proj_b2"] = {
+                "fused_us": round(us_fu2 * 1e3, 2),
+                "fused_TFLOP/s": round(2 * gemm_flops / (us_fu2 * 1e-3) / 1e12, 1),
+                "linear_plus_prologue_us": round(us_sp2 * 1e3, 2),
+                "what": "qkv_proj_norm_rope vs F.linear (hipBLASLt) + qkv_norm_rope, B=2, 4096 tokens",
+            }
+            del hid, hid2, wq
 
             # Cross-attention projections at config 3 (B=2, 4096 image tokens,
             # 512 text tokens of width 1024): xq + head_norm and xkv + the key
