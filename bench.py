@@ -134,7 +134,7 @@ def copy_calibration(dev) -> None:
 
 
 PROFILE_CASES = ("self_cfg2", "self_cfg1", "prologue_cfg2", "head_norm_cfg3", "cross_cfg3",
-                 "cross_b2_512", "rowquant_cfg3", "prologue_bwd_cfg5", "vae_d384", "qkv_proj_cfg2",
+                 "cross_b2_512", "rowquant_cfg3", "prologue_bwd_cfg5", "vae_d384", "qkv_proj_cfg2", "qkv_proj_b2",
                  "xq_proj_cfg3", "xkv_proj_cfg3", "fwd_bwd_cfg5")
 
 
@@ -187,12 +187,12 @@ def profile_case(name: str, steps: int, pkg, fp8, dev) -> dict:
         else:
             o_att = torch.randn(2, S, H * d, generator=g).to(dev, BF)
             fn = lambda: fp8.rowquant(o_att)
-    elif name in ("qkv_proj_cfg2", "xq_proj_cfg3", "xkv_proj_cfg3"):
+    elif name in ("qkv_proj_cfg2", "qkv_proj_b2", "xq_proj_cfg3", "xkv_proj_cfg3"):
         proj = importlib.import_module("anima_flat_amd.kernels.proj")
         p = prologue_qkv(pkg, B, S, H, 1002, dev)
         D = H * d
-        if name == "qkv_proj_cfg2":
-            hid = torch.randn(B, S, D, generator=g).to(dev, BF)
+        if name in ("qkv_proj_cfg2", "qkv_proj_b2"):
+            hid = torch.randn(2 if name == "qkv_proj_b2" else B, S, D, generator=g).to(dev, BF)
             wq = (torch.randn(3 * D, D, generator=g) * D**-0.5).to(dev, BF)
             fn = lambda: proj.qkv_proj_norm_rope(hid, wq, p["q_weight"], p["k_weight"], p["cos"], p["sin"], H, eps)
         elif name == "xq_proj_cfg3":
