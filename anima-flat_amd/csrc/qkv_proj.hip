@@ -362,6 +362,10 @@ static int launch_proj(const char* what, const void* hid, int64_t hid_row_stride
   if (K <= 0 || K % kPKMin != 0 || K > (1 << 20))
     return fail(AA_EUNSUPPORTED, w + ": the input width must be a positive multiple of 32");
   if (B * S == 0) return AA_OK;
+  // The DMA's per-lane byte offsets within an 8-row block are 32-bit:
+  // 7 rows x stride x 2 bytes must stay below 2^32.
+  if (hid_row_stride > (int64_t(1) << 27))
+    return fail(AA_EUNSUPPORTED, w + ": input row stride must be at most 2^27 elements");
   if (!hid || !weight) return fail(AA_EINVAL, w + ": null pointer");
   bool any_rope = false;
   for (int g = 0; g < nseg; ++g) {

@@ -86,7 +86,7 @@ int aa_qkv_norm_rope_fwd(const void* qkv, void* q, void* k, void* v,
  * QKV projection fused with the prologue: q, k, v = aa_qkv_norm_rope_fwd of
  * qkv = hid @ weight^T (bf16), without qkv ever reaching memory.
  *   hid [B*S rows, H*hd], row r at hid + r * hid_row_stride elements
- *   (hid_row_stride >= H*hd, a multiple of 8); weight [3*H*hd, H*hd]
+ *   (hid_row_stride >= H*hd, a multiple of 8, at most 2^27); weight [3*H*hd, H*hd]
  *   contiguous (nn.Linear layout, no bias); q, k, v [B, S, H, hd] contiguous
  *   outputs (v is the projection's V section as it is); q_weight, k_weight,
  *   cos, sin as for aa_qkv_norm_rope_fwd. H <= 64.
@@ -104,7 +104,7 @@ int aa_qkv_proj_norm_rope(const void* hid, int64_t hid_row_stride, const void* w
  * A projection fused with per-head RMSNorm: y = aa_head_norm_fwd of
  * x @ weight^T (bf16), the projection never reaching memory.
  *   x [B*S rows, K], row r at x + r * x_row_stride elements (x_row_stride >= K,
- *   a multiple of 8; K a multiple of 32); weight [H*hd, K] contiguous (nn.Linear
+ *   a multiple of 8, at most 2^27; K a multiple of 32); weight [H*hd, K] contiguous (nn.Linear
  *   layout, no bias); y [B, S, H, hd] contiguous; norm_weight [hd] float32.
  * Replaces: src/model.py:324 (b.xq(hid), model.py:138, followed by head_norm,
  *           src/kernels/rope.py:648-652) on the inference path.

@@ -121,6 +121,8 @@ def test_invalid_arguments_fail_before_any_launch(pkg, lib):
     assert proj(65, 128, 0) == L.AA_EINVAL  # H > 64
     assert proj(2, 128, 0) == L.AA_EINVAL  # null pointers
     assert proj(2, 128, 0, B=0) == L.AA_OK  # no tokens: nothing to do
+    assert proj(2, 128, 0, rs=(1 << 27) + 8) == L.AA_EUNSUPPORTED  # 32-bit DMA offsets
+    assert "row stride" in lib.aa_last_error().decode()
     xq = lambda hd, K, B=1: lib.aa_proj_head_norm(None, 256, None, K, None, None, B, 4, 2, hd, 1e-6, 0, None)
     assert xq(96, 256) == L.AA_EUNSUPPORTED  # head_dim
     assert xq(128, 80) == L.AA_EUNSUPPORTED  # K % 32
