@@ -76,8 +76,8 @@ struct Params {
 //   phase 2t   : A runs M_A(t), B runs X_B(t-1)
 //   phase 2t+1 : A runs X_A(t), B runs M_B(t)
 // so on every SIMD one wave's MFMAs overlap the other wave's VALU work.
-// Only the Q and dO rows of each query tile come into LDS (swizzled row
-// tiles, tile_io.h) with its stats record, in a 4-stage ring: the S / dP A
+// Only the Q and dO rows of each query tile come into LDS (dual line tiles,
+// tile_io.h) with its stats record, in a 4-stage ring: the S / dP A
 // operands are 16-byte row reads, the dV / dK A operands (dO^T, Q^T of the
 // previous tile) are pairs of ds_read_b64_tr_b16 transposed reads of the same
 // tiles. The B waves DMA tile t+2 at the start of X_B(t-1) (phase 2t); it is
@@ -292,7 +292,7 @@ void dkdv_kernel(Params p, int nkblk, int total_blocks) {
 // Waves 0-3 (group A) and 4-7 (group B) run the same stream one phase apart
 // (B executes one extra barrier first, A one at the end):
 //   phase 2t: A runs M(t), B runs X(t-1);  phase 2t+1: A runs X(t), B runs M(t)
-// K and V rows stream into a 4-stage ring of swizzled row tiles (tile_io.h):
+// K and V rows stream into a 4-stage ring of dual line tiles (tile_io.h):
 // group A DMAs tile t+2 at the start of X(t) (phase 2t+1) into the stage of
 // tile t-2 (last read in phase 2t-1) and waits for tile t+1 at its end.
 constexpr int kDqWaves = 8;                  // two per SIMD

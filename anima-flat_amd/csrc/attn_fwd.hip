@@ -9,7 +9,7 @@
 //   (schedule at the kernel).
 //
 // Transposed formulation (per wave, per 64-key tile)
-//   S^T = K Q^T   : A = K rows from the LDS row tile (32 keys x 16 d per
+//   S^T = K Q^T   : A = K rows from the LDS line tile (32 keys x 16 d per
 //                   MFMA), B = Q^T from registers (loaded once).
 //   O^T += V^T P^T: A = V^T (32 d x 16 keys), read transposed from the LDS
 //                   V rows, B = P^T from the S^T accumulators.
@@ -20,10 +20,11 @@
 //   output rescale is a per-lane scalar multiply.
 //
 // K/V staging (tile_io.h): K and V rows are copied HBM -> LDS by DMA
-//   (global_load_lds_dwordx4), K into the row-tile layout (16-byte
-//   ds_read_b128 operand reads), V into the swizzled row-tile layout, whose
-//   V^T operands are pairs of ds_read_b64_tr_b16 transposed reads. Both are
-//   free of bank conflicts.
+//   (global_load_lds_dwordx4) into line tiles, blocks of 8 rows x 64 d that
+//   one DMA instruction fills from 8 whole 128-byte lines; the 16-byte chunk
+//   XOR differs: K's suits its 16-byte ds_read_b128 operand reads, V's its
+//   V^T operands, pairs of ds_read_b64_tr_b16 transposed reads. Both are free
+//   of bank conflicts.
 //
 // Q and O staging: each wave's 32 Q rows come in by DMA (4 rows x 256 B per
 //   instruction) into ring stages that the first tiles do not use, and are

@@ -2,7 +2,9 @@
 //
 // Every streamed operand is a tile of 64 rows x 128 bf16 (16 KB): 64 keys or
 // queries, each with its 128 head-dim values. LDS has 64 banks of 4 bytes;
-// both formats below keep every operand read free of bank conflicts.
+// every format below keeps its operand reads free of bank conflicts. The
+// row tiles serve the head_dim-384 forward (32-row sub-tiles); the line tiles
+// further down serve the head_dim-128 forward and the backward.
 //
 // Row tile: element (r, d) at (r >> 4) * 2048 + (d >> 3) * 128 + (r & 15) * 8 + (d & 7),
 //   i.e. 256-byte slices of (16-row group, 16-byte chunk). An A-operand read
@@ -12,10 +14,9 @@
 // Swizzled row tile: the same with the row slot inside each slice XORed with
 //   4 * (chunk % 4): element (r, d) at
 //   (r >> 4) * 2048 + (d >> 3) * 128 + (((r & 15) ^ (4 * ((d >> 3) & 3))) * 8) + (d & 7).
-//   Row-operand reads stay conflict free (swz_row_rd), and the tile can also
-//   be read transposed with ds_read_b64_tr_b16 (swz_tr_rd, read_tr_operand):
-//   the 32 lanes of one read touch 4 rows x 4 chunks, which land in 16
-//   distinct slots.
+//   It can be read transposed with ds_read_b64_tr_b16 (swz_tr_rd): the 32
+//   lanes of one read touch 4 rows x 4 chunks, which land in 16 distinct
+//   slots.
 //
 // Transposed operand: the A operand of v_mfma_f32_32x32x16_bf16 with the
 //   tile's rows as the k index, A[m][k] = tile(row k, column 32 dt + m) for
@@ -41,13 +42,6 @@ constexpr int kTileElems = kTileRows * 128;  // 16 KB of bf16
 __device__ __forceinline__ int row_rd(int lane) {
   const int li = lane & 31, hh = lane >> 5;
   return (li >> 4) * 2048 + (li & 15) * 8 + hh * 128;
-}
-
-// Per-lane read offset of a row-operand read of a swizzled row tile: row
-// 32 t + li, chunk 2 kk + hh is at swz_row_rd(lane, kk & 1) + 4096 t + 256 kk.
-__device__ __forceinline__ int swz_row_rd(int lane, int kk_odd) {
-  const int li = lane & 31, hh = lane >> 5;
-  return (li >> 4) * 2048 + hh * 128 + (((li & 15) ^ (8 * kk_odd + 4 * hh)) * 8);
 }
 
 // Per-lane offsets of the two ds_read_b64_tr_b16 reads (r2 = 0, 1) of a
@@ -95,22 +89,6 @@ __device__ __forceinline__ void dma16_off(const void* src, const void* lds_base)
 
 __device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-// DMA blocks 4 g .. 4 g + 3 of a swizzled row tile whose row 0 is at `base`
-// (row stride rs elements): rows 16 g + ((lane & 15) ^ (4 lq)), lq = lane >> 4,
-// chunk 4 i + lq for block 4 g + i. The four blocks read the same rows, so
-// they share one address with immediate offsets of 64 i bytes. Rows at or
-// past `nrows` (>= 1) re-read row nrows - 1, finite data the caller masks.
-__device__ __forceinline__ void dma_row_quad_swz(const bf16* base, int64_t rs, int nrows,
-                                                 const bf16* lds_tile, int g, int lane) {
-  const int row = min(16 * g + ((lane & 15) ^ (4 * (lane >> 4))), nrows - 1);
-  const bf16* src = base + (int64_t)row * rs + 8 * (lane >> 4);
-  const bf16* dst = lds_tile + 4 * g * 512;
-  dma16_off<0>(src, dst);
-  dma16_off<64>(src, dst + 512);
-  dma16_off<128>(src, dst + 1024);
-  dma16_off<192>(src, dst + 1536);
-}
-
 // Transposed operand reads ---------------------------------------------------
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
@@ -139,16 +117,6 @@ __device__ __forceinline__ bf16x8 lds_ld16(uint32_t addr) {
 // ds_read_b64_tr_b16 at an LDS byte address.
 __device__ __forceinline__ s16x4 lds_ld8_tr(uint32_t addr) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(uintptr_t)addr);
-}
-
-// Transposed operand (dt, c4) of a swizzled row tile; tr0 / tr1 are
-// swz_tr_rd(lane, 0 / 1).
-__device__ __forceinline__ bf16x8 read_tr_operand(const bf16* tile, int c4, int dt, int tr0,
-                                                  int tr1) {
-  const bf16* base = tile + 2048 * c4 + 512 * dt;
-  const s16x4 lo = ds_read_tr(base + tr0);
-  const s16x4 hi = ds_read_tr(base + tr1);
-  return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
 // Line tile (the forward's K and V) -------------------------------------------
