@@ -64,3 +64,51 @@ def test_graph_replays_match_eager(pkg, fp8, proj):
             torch.cuda.synchronize()
             for a, e in zip(outs, eager):
                 assert torch.equal(a, e), f"replay {i}: {a.dtype} {tuple(a.shape)} differs"
+
+
+def test_graph_replays_split_backward_and_projections(pkg, proj):
+    """The launches the first test leaves out: the key-split forward (64 work
+    items of 256 queries on the chip's CUs: partials in a workspace, then the
+    combine pass), the backward (dq then dkdv, stats in a workspace), the
+    cross-attention projections and the head_dim-384 forward (split as well)."""
+    vae = pkg.vae
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(91)
+    d = 128
+    q1, k1, v1 = (ref.bf16_normal((1, 1024, 16, d), g).to(dev, BF) for _ in range(3))
+    qb, kb, vb = (ref.bf16_normal((1, 320, 2, d), g).to(dev, BF) for _ in range(3))
+    dout = ref.bf16_normal((1, 320, 2, d), g).to(dev, BF)
+    xq = ref.bf16_normal((2, 200, 512), g).to(dev, BF)
+    wq = (torch.randn(4 * d, 512, generator=g) * 512**-0.5).to(dev, BF)
+    nw = ref.norm_weight(d, g).to(dev)
+    ctx = ref.bf16_normal((2, 77, 256), g).to(dev, BF)
+    wkv = (torch.randn(2 * 4 * d, 256, generator=g) * 256**-0.5).to(dev, BF)
+    q3, k3, v3 = (ref.bf16_normal((1, 1, 1024, 384), g).to(dev, BF) for _ in range(3))
+
+    def step():
+        o1 = torch.ops.anima_flat.fa_fwd_nolse(q1, k1, v1)
+        ob, lse = torch.ops.anima_flat.fa_fwd(qb, kb, vb)
+        dq, dk, dv = torch.ops.anima_flat.fa_bwd(dout, qb, kb, vb, ob, lse)
+        y = proj.proj_head_norm(xq, wq, nw, 4, 1e-6)
+        kk, vv = proj.kv_proj_norm(ctx, wkv, nw.to(BF), 4, 1e-6)
+        o3 = vae.attend(q3, k3, v3)
+        return [o1, ob, lse, dq, dk, dv, y, kk, vv, o3]
+
+    with torch.no_grad():
+        eager = [t.clone() for t in step()]
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            step()
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            outs = step()
+        for i in range(3):
+            # eager launches of the same kernels on other shapes in between
+            torch.ops.anima_flat.fa_fwd_nolse(*(ref.bf16_normal((1, 700, 3, d), g).to(dev, BF) for _ in range(3)))
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            for j, (a, e) in enumerate(zip(outs, eager)):
+                assert torch.equal(a, e), f"replay {i}: output {j} {a.dtype} {tuple(a.shape)} differs"
