@@ -502,6 +502,12 @@ __global__ __launch_bounds__(256) void attn_fwd_combine_kernel(FwdParams p) {
   if (qrow >= p.Sq) return;
   const int d0 = 8 * (threadIdx.x & 15);
   const int64_t row0 = (int64_t)j * p.nsplit;
+  // Every load (the splits' O rows and LSEs) goes out before any is used:
+  // one memory round trip instead of one per split.
+  u32x4 raw[8];
+#pragma unroll
+  for (int s = 0; s < 8; ++s)
+    if (s < p.nsplit) raw[s] = ld16(p.part_o + ((row0 + s) * kQPerWg + qloc) * kD + d0);
   float ls[8];
   float mx = -INFINITY;
 #pragma unroll
@@ -518,10 +524,12 @@ __global__ __launch_bounds__(256) void attn_fwd_combine_kernel(FwdParams p) {
     lse = mx + logf(sum);
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
+      // A range with no keys left its partial unwritten: skipped, not
+      // weighted by 0 (its bytes may hold NaN).
       if (s < p.nsplit && ls[s] > -INFINITY) {
         const float wgt = expf(ls[s] - lse);
         float v[8];
-        unpack8(ld16(p.part_o + ((row0 + s) * kQPerWg + qloc) * kD + d0), v);
+        unpack8(raw[s], v);
 #pragma unroll
         for (int i = 0; i < 8; ++i) acc[i] = fmaf(wgt, v[i], acc[i]);
       }

@@ -502,6 +502,11 @@ __global__ __launch_bounds__(192) void attn_fwd_d384_combine_kernel(Params p) {
   if (qrow >= p.Sq) return;
   const int d0 = 8 * ((int)threadIdx.x % 48);
   const int64_t rec0 = (int64_t)item * p.nsplit;
+  // Every load goes out before any is used (one memory round trip).
+  u32x4 raw[kMaxSplit];
+#pragma unroll
+  for (int s = 0; s < kMaxSplit; ++s)
+    if (s < p.nsplit) raw[s] = ld16(p.part_o + ((rec0 + s) * kQPerWg + qloc) * kD + d0);
   float ls[kMaxSplit];
   float mx = -INFINITY;
 #pragma unroll
@@ -521,7 +526,7 @@ __global__ __launch_bounds__(192) void attn_fwd_d384_combine_kernel(Params p) {
       if (s < p.nsplit && ls[s] > -INFINITY) {
         const float wgt = expf(ls[s] - lse);
         float v[8];
-        unpack8(ld16(p.part_o + ((rec0 + s) * kQPerWg + qloc) * kD + d0), v);
+        unpack8(raw[s], v);
 #pragma unroll
         for (int i = 0; i < 8; ++i) acc[i] = fmaf(wgt, v[i], acc[i]);
       }
