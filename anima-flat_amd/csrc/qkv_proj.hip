@@ -195,8 +195,9 @@ __global__ __launch_bounds__(T::kThreads) void qkv_proj_kernel(ProjParams p) {
   // their MFMAs: those of the first kPre steps before the next stage's DMA
   // starts going out (its asm is a compiler memory barrier, so they cannot
   // sink to their MFMAs), the rest kPre steps ahead. The DMA goes out in
-  // kDmaParts parts, one at the start of each of the first k-steps. With 192 accumulator registers (kCB = 6) only one
-  // k-step's operands fit beside them at two waves per SIMD.
+  // kDmaParts parts, one at the start of each of the first k-steps. With 192
+  // accumulator registers (kCB = 6) only one k-step's operands fit beside
+  // them at two waves per SIMD.
   constexpr int kPre = T::kCB <= 4 ? 2 : 1;
   auto stage = [&](int s, auto nsteps) {
     constexpr int NSTEPS = decltype(nsteps)::value;
