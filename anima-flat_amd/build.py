@@ -44,8 +44,14 @@ DEVICE_FLAGS = [
 
 RESOURCE_REMARK = "-Rpass-analysis=kernel-resource-usage"
 
-# Per-source extra flags (none at present).
-SOURCE_FLAGS: dict[str, list[str]] = {}
+# Per-source extra flags. attn_fwd.hip runs one wave per SIMD, where the
+# compiler would otherwise give every MFMA accumulator the AGPR file; its
+# score accumulators must be VGPRs (the softmax reads them), so the builtin
+# MFMAs are compiled in the VGPR form and the output accumulators are pinned to
+# AGPRs through inline asm.
+SOURCE_FLAGS: dict[str, list[str]] = {
+    "attn_fwd.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+}
 
 
 def hipcc() -> str:

@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <string>
+#include <type_traits>
 
 #include "../../include/anima_attn.h"
 
@@ -107,6 +108,17 @@ __device__ __forceinline__ float group_sum(float x) {
 
 __device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// f(std::integral_constant<int, i>) for i = B .. E - 1, unrolled at compile
+// time (the slot schedules of the attention kernels index registers and pick
+// work per slot with it).
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
 }
 
 // ------------------------------------------------------------------ host --

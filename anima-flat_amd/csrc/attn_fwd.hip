@@ -2,22 +2,38 @@
 // for gfx950 (CDNA4): v_mfma_f32_32x32x16_bf16 for both products.
 //
 // Work decomposition
-//   One workgroup = 8 waves = 256 queries of one (batch, head). Each wave
-//   owns 32 queries for the whole kernel; K/V tiles of 64 keys are streamed
-//   into a 4-stage LDS ring and shared by the 8 waves. The waves run in two
-//   phase-shifted groups so that MFMA and softmax work overlap on every SIMD
-//   (schedule at the kernel).
+//   One workgroup = 4 waves, one per SIMD, = 256 queries of one (batch,
+//   head). Each wave owns 64 queries (two blocks of 32) for the whole key
+//   range; K/V tiles of 64 keys stream through a 4-stage LDS ring that the 4
+//   waves share. Every K or V^T operand a wave reads from LDS feeds two MFMAs
+//   (one per query block): 0.5 KB of LDS reads per MFMA.
 //
-// Transposed formulation (per wave, per 64-key tile)
+// Why one wave per SIMD with 64 queries: a 32x32x16 MFMA holds up the
+//   SIMD's issue of other vector work for about 20 of the 32 cycles it keeps
+//   the matrix pipe busy, so a tile costs the SIMD roughly the sum of its MFMA,
+//   softmax VALU and LDS-read issue time, whichever wave issues them. With 32
+//   queries per wave (two waves per SIMD) every MFMA needed its own 1 KB
+//   operand, two LDS reads; with 64 queries the same operand serves two
+//   MFMAs, which removes a quarter of the per-tile issue time.
+//
+// Transposed formulation (per wave, per 64-key tile, per query block qb)
 //   S^T = K Q^T   : A = K rows from the LDS line tile (32 keys x 16 d per
 //                   MFMA), B = Q^T from registers (loaded once).
 //   O^T += V^T P^T: A = V^T (32 d x 16 keys), read transposed from the LDS
 //                   V rows, B = P^T from the S^T accumulators.
 //   The 32x32 accumulator layout puts column j = lane%32 in every lane, with
 //   rows 8*(r/4) + 4*(lane/32) + r%4 in register r. With queries as columns,
-//   every lane holds one query: the softmax row max/sum are in-lane
-//   reductions plus one v_permlane32_swap with the partner lane, and the
-//   output rescale is a per-lane scalar multiply.
+//   every lane holds one query of each block: the softmax row max/sum are
+//   in-lane reductions plus one v_permlane32_swap with the partner lane, and
+//   the output rescale is a per-lane scalar multiply.
+//
+// Slot schedule: a tile is 64 slots of one MFMA each; the other work of the
+//   tile is dealt to fixed slots and held there by sched_barrier:
+//     slots  0-31: S^T of tile t+1 (QK)     | P of tile t (fma, exp, bf16, sums)
+//     slots 32-63: O^T += V^T P^T of tile t | the rest of P, then the row max
+//                                             of tile t+1
+//   then the (rare) lazy rescale when tile t+1 raised a row max. The K/V DMA of
+//   tile t+3 is issued one instruction per slot in the first half.
 //
 // K/V staging (tile_io.h): K and V rows are copied HBM -> LDS by DMA
 //   (global_load_lds_dwordx4) into line tiles, blocks of 8 rows x 64 d that
@@ -26,13 +42,10 @@
 //   V^T operands, pairs of ds_read_b64_tr_b16 transposed reads. Both are free
 //   of bank conflicts.
 //
-// Q and O staging: each wave's 32 Q rows come in by DMA (4 rows x 256 B per
+// Q and O staging: each wave's 64 Q rows come in by DMA (4 rows x 256 B per
 //   instruction) into ring stages that the first tiles do not use, and are
-//   read into the Q^T registers from there; O leaves the same way, written to
-//   free ring stages and stored 4 whole rows per instruction. (Loading and
-//   storing straight from the accumulator layout touches 32 rows x 16-32 B
-//   per instruction; staging cut the fixed cost of a round of work items by
-//   about 5 us.)
+//   read into the Q^T registers from there; O leaves the same way through the
+//   ring after the last tile, 4 whole rows per store.
 //
 // Key order of P^T
 //   The B operand of the MFMA wants, in lane l, 8 consecutive k-indices
@@ -46,7 +59,7 @@
 //   p = exp2(s*c - m*c) with c = scale * log2(e), one FMA and one v_exp_f32
 //   per score. m is only raised when a tile's max exceeds it by more than
 //   8/c (8 in log2 units), so p <= 256 and the O/l rescale (a pass over the
-//   64 accumulator registers) runs only a few times per row. The row sum is
+//   128 accumulator registers) runs only a few times per row. The row sum is
 //   taken over the bf16-rounded P that feeds the MFMA, with v_dot2c_f32_bf16.
 #include <algorithm>
 #include <atomic>
@@ -62,8 +75,15 @@
 namespace aa {
 
 constexpr int kD = 128;
-constexpr int kBN = 64;                     // keys per tile
-constexpr float kRescaleThreshold = 8.0f;   // log2 units
+constexpr int kBN = 64;                      // keys per tile
+constexpr float kRescaleThreshold = 8.0f;    // log2 units
+constexpr int kWaves = 4;                    // one per SIMD
+constexpr int kQPerWave = 64;                // two blocks of 32 queries
+constexpr int kQPerWg = kWaves * kQPerWave;  // 256 queries per work item
+constexpr int kStages = 4;                   // K/V ring depth (4 x 32 KB)
+constexpr int kLead = kStages - 1;           // tile t + kLead is fetched during tile t
+constexpr uint32_t kStageBytes = 2u * kTileElems * sizeof(bf16);  // K tile, then V tile
+constexpr uint32_t kVOff = kTileElems * sizeof(bf16);             // V tile in a stage
 
 struct FwdParams {
   const bf16* q;
@@ -91,27 +111,6 @@ struct FwdParams {
   float* part_lse;
 };
 
-__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
-
-// All but the newest n tiles of this wave's DMA complete (8 instructions per
-// tile for a group-A wave: 4 K + 4 V). n is wave-uniform, 0..3.
-__device__ __forceinline__ void wait_dma_tiles_in_flight(int n) {
-  switch (n) {
-    case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
-    case 1: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
-    case 2: asm volatile("s_waitcnt vmcnt(16)" ::: "memory"); break;
-    default: asm volatile("s_waitcnt vmcnt(24)" ::: "memory"); break;
-  }
-}
-
-constexpr int kWaves = 8;    // two groups of 4, one wave of each group per SIMD
-constexpr int kDmaWaves = 4; // group A issues every DMA
-constexpr int kStages = 4;   // K/V ring depth (4 x 32 KB)
-constexpr int kAhead = kStages - 2;  // tiles of DMA in flight beyond the next one
-constexpr int kQPerWg = kWaves * 32;
-constexpr int kDmaPerWave = 16 / kDmaWaves;  // 1 KB DMA blocks per group-A wave per tile, K and V each
-static_assert(2 * kDmaPerWave == 8, "the DMA waits count 8 instructions per tile");
-
 // (batch, head, query block) of one work item; klen keys attended.
 struct Item {
   int b, h, qblk, klen, ntiles;
@@ -128,277 +127,443 @@ __device__ __forceinline__ Item decode_item(const FwdParams& p, int it) {
   return r;
 }
 
-// K/V tile DMA of one group-A wave into K and V line tiles (tile_io.h). A DMA
-// instruction fills one 1 KB block = 8 rows x 64 d from 8 whole 128-byte
-// lines; wave w fills blocks 4 w .. 4 w + 3: d-half w >> 1, rows
-// 32 (w & 1) + 8 i + (lane >> 3) for i = 0..3. Full tiles use a scalar row
-// base per instruction and a 32-bit per-lane offset. Rows past klen (last
-// tile only) re-read row klen-1: finite data whose scores are masked to
-// -inf, so their P is 0.
+// K/V tile DMA of one wave into the K and V line tiles of a ring stage
+// (tile_io.h). A DMA instruction fills one 1 KB block = 8 rows x 64 d from 8
+// whole 128-byte lines; wave w fills blocks 4 w .. 4 w + 3 of the K tile and
+// of the V tile: d-half w >> 1, rows 32 (w & 1) + 8 i + (lane >> 3),
+// i = 0..3. A job (one tile) takes one scalar base per tensor (the tile's
+// first row) and per-lane 32-bit byte offsets that hold each lane's row and
+// column, so its instructions need no address arithmetic. Rows at or past Sk
+// re-read row Sk - 1: finite data, and rows at or past the key length have
+// their scores masked to -inf (P = 0).
 struct KVDma {
-  int b0, rw, rbase, kcol0, kcol1, vcol;  // rw: the wave's first row (uniform)
-  uint32_t koff0, koff1, voff;
+  uint32_t ko[4], vo[4];      // per-lane offsets of blocks 0-3 (those of a tile inside Sk
+                              // unless `clamped`)
+  bool clamped;
+  const bf16* kbase;          // this job's scalar bases
+  const bf16* vbase;
+  uint32_t dst;               // LDS byte address of this job's first K block
 
-  __device__ __forceinline__ void setup(const FwdParams& p, int wave, int lane) {
-    b0 = wave * kDmaPerWave;
-    rw = 32 * (wave & 1);
-    rbase = rw + (lane >> 3);
-    const int h64 = 64 * (wave >> 1);
-    kcol0 = h64 + 8 * line_k_chunk(lane, 0);
-    kcol1 = h64 + 8 * line_k_chunk(lane, 1);
-    vcol = h64 + 8 * line_v_chunk(lane);
-    const int r = lane >> 3;
-    koff0 = (uint32_t)(r * p.ks1 + kcol0) * 2u;
-    koff1 = (uint32_t)(r * p.ks1 + kcol1) * 2u;
-    voff = (uint32_t)(r * p.vs1 + vcol) * 2u;
+  __device__ __forceinline__ static int row_of(int wave, int i, int lane) {
+    return 32 * (wave & 1) + 8 * i + (lane >> 3);
+  }
+  __device__ __forceinline__ static int kcol(int wave, int i, int lane) {
+    return 64 * (wave >> 1) + 8 * line_k_chunk(lane, i & 1);
+  }
+  __device__ __forceinline__ static int vcol(int wave, int lane) {
+    return 64 * (wave >> 1) + 8 * line_v_chunk(lane);
   }
 
-  // Tile t (keys 64 t ..) of the (batch, head) at kp / vp into kd / vd.
-  __device__ __forceinline__ void issue(const FwdParams& p, const bf16* kp, const bf16* vp, int klen,
-                                        int t, bf16* kd, bf16* vd) const {
-    const int kb = t * kBN;
-    static_assert(kDmaPerWave == 4, "four DMA blocks per wave per tile");
-    if (kb + kBN <= klen) {
+  __device__ __forceinline__ void fixed(const FwdParams& p, int wave, int lane) {
 #pragma unroll
-      for (int i = 0; i < kDmaPerWave; ++i) {
-        const int row0 = kb + rw + 8 * i;
-        dma16_sv(vp + (int64_t)row0 * p.vs1, voff, vd + (b0 + i) * 512);
-      }
-#pragma unroll
-      for (int i = 0; i < kDmaPerWave; ++i) {
-        const int row0 = kb + rw + 8 * i;
-        dma16_sv(kp + (int64_t)row0 * p.ks1, (i & 1) ? koff1 : koff0, kd + (b0 + i) * 512);
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < kDmaPerWave; ++i) {
-        const int r = min(kb + rbase + 8 * i, klen - 1);
-        dma16(vp + (int64_t)r * p.vs1 + vcol, vd + (b0 + i) * 512);
-      }
-#pragma unroll
-      for (int i = 0; i < kDmaPerWave; ++i) {
-        const int r = min(kb + rbase + 8 * i, klen - 1);
-        dma16(kp + (int64_t)r * p.ks1 + ((i & 1) ? kcol1 : kcol0), kd + (b0 + i) * 512);
-      }
+    for (int i = 0; i < 4; ++i) {
+      const int r = row_of(wave, i, lane);
+      ko[i] = (uint32_t)(r * p.ks1 + kcol(wave, i, lane)) * 2u;
+      vo[i] = (uint32_t)(r * p.vs1 + vcol(wave, lane)) * 2u;
     }
+    clamped = false;
+  }
+  __device__ __forceinline__ void setup(const FwdParams& p, int wave, int lane) {
+    fixed(p, wave, lane);
+  }
+
+  // The job of the tile whose first key row is kbrow (when real), else a
+  // dummy job that moves rows from 0 into the same stage, which nothing reads
+  // again: every tile then issues the same number of DMA instructions and one
+  // vmcnt serves every wait. Only a tile that reaches past Sk (or a dummy job
+  // with Sk < 64) needs clamped offsets.
+  __device__ __forceinline__ void prepare(const FwdParams& p, bool real, int kbrow, uint32_t stage,
+                                          int wave, const bf16* kp, const bf16* vp, int lane) {
+    const int row0 = real ? kbrow : 0;
+    dst = stage + (uint32_t)(4 * wave) * 1024u;
+    if (row0 + kBN <= p.Sk) {
+      kbase = kp + (int64_t)row0 * p.ks1;
+      vbase = vp + (int64_t)row0 * p.vs1;
+      if (clamped) fixed(p, wave, lane);
+    } else {
+      const int last = p.Sk - 1;
+      const int rs = min(row0, last);
+      kbase = kp + (int64_t)rs * p.ks1;
+      vbase = vp + (int64_t)rs * p.vs1;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = min(row0 + row_of(wave, i, lane), last) - rs;
+        ko[i] = (uint32_t)(r * p.ks1 + kcol(wave, i, lane)) * 2u;
+        vo[i] = (uint32_t)(r * p.vs1 + vcol(wave, lane)) * 2u;
+      }
+      clamped = true;
+    }
+  }
+
+  // DMA instruction i of the job: 0-3 the K blocks, 4-7 the V blocks.
+  template <int i>
+  __device__ __forceinline__ void issue() const {
+    constexpr uint32_t off = (i < 4 ? 0u : kVOff) + (uint32_t)(i & 3) * 1024u;
+    if constexpr (i < 4) dma16_sva(kbase, ko[i & 3], dst + off);
+    else dma16_sva(vbase, vo[i & 3], dst + off);
   }
 };
 
-// Per-wave state and work of the forward: 32 queries, their Q^T operands,
-// O^T accumulators and running softmax statistics.
-struct FwdWave {
-  bf16x8 qreg[8];  // Q^T operand: lane holds Q[query li][16 kk + 8 hh + 0..7]
-  f32x16 o[4];     // O^T, d = 32 dt + rows
-  // Running max in raw score units (before the scale); l partial sums in
-  // four independent chains.
-  float m_raw;
-  float l4[4];
-  f32x16 s0, s1;  // S^T of the tile between its M and X blocks
-  bf16x8 pb[4];   // P^T of the tile between its X block and the next M block
-  int hh, li;
-  int k_rd[4];  // line_k_rd(lane, j)
-  int v_tr[2];  // line_v_tr(lane, dt & 1)
-  float c, thr_raw;
+// Operand reads ahead of their MFMA: K operands (each feeds the two MFMAs of
+// a pair of slots) are read kKPf pairs ahead, V^T operands kVPf pairs ahead
+// into a queue one entry longer than that needs (a V^T operand stays
+// allocated for one slot after its last MFMA).
+constexpr int kKPf = 2, kKQ = kKPf + 1;
+constexpr int kVPf = 2, kVQ = kVPf + 2;
+constexpr int kread_slot(int j) { return j < kKPf ? 0 : 2 * (j - kKPf); }
+constexpr int vread_slot(int pp) { return 32 + 2 * (pp - kVPf); }
+// P unit u (2 scores of query block (u >> 2) & 1, key chunk u >> 3) starts in
+// slot 3u / 2 and ends two slots later (slots 0-48); the P operand of chunk c4
+// is first used in slot 32 + 8 c4, after its last unit. Max steps of the next
+// tile: slots 48-63.
+constexpr int exp_slot(int u) { return (3 * u) / 2; }
+constexpr int kMaxSlot0 = 48;
+// DMA instruction i of the tile's job: slot 4 i + 3.
+constexpr int dma_slot(int i) { return 4 * i + 3; }
 
-  __device__ __forceinline__ void setup(int lane, float c_) {
+// O^T += V^T P^T with O in AGPRs, as inline asm: the builtin would follow the
+// function-wide choice of one register file for every MFMA accumulator, and S
+// must stay in VGPRs for the softmax. O is only read or written by VALU code
+// behind fence_o(), and the A/B operands are read when the MFMA issues.
+__device__ __forceinline__ void mfma_pv(f32x16& acc, bf16x8 a, bf16x8 b) {
+  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+__device__ __forceinline__ void keep_alive(bf16x8 v) { asm volatile("" ::"v"(v)); }
+// Row sums (the accumulator and the 0/1 selector in AGPRs, as for O).
+__device__ __forceinline__ void mfma_rowsum(f32x4& acc, bf16x8 sel, bf16x8 p) {
+  asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc) : "a"(sel), "v"(p));
+}
+
+// Per-wave state and work: 64 queries (blocks qb = 0, 1 of 32), their Q^T
+// operands, O^T accumulators and running softmax statistics.
+struct FwdWave {
+  bf16x8 qreg[2][8];  // Q^T (qb, kk): lane holds Q[32 qb + li][16 kk + 8 hh + 0..7]; AGPRs
+  f32x16 o[4][2];     // O^T (dt, qb): d = 32 dt + rows, query 32 qb + li; AGPRs
+  f32x16 s[2][2][2];  // S^T (buffer, kb, qb): keys 32 kb + rows of the tile, query 32 qb + li
+  bf16x8 pb[4][2];    // P^T (c4, qb): keys 16 c4 + .. of the tile, in accumulator order
+  float m_raw[2];     // running max of query 32 qb + li, raw score units
+  float mt[2];        // row max of the next tile (raw)
+  f32x4 lsum[2];      // row sum of query 32 qb + li (all four elements), by MFMA
+  bf16x8 sel;         // 0/1 selector: the A operand of the row-sum MFMA
+  float c, thr_raw;
+  int li, hh;
+  uint32_t kb4[4];  // LDS byte address of this lane's K operand reads in the next tile's K
+                    // (line_k_rd(lane, j)); advanced one stage per tile
+  uint32_t vb2[2];  // ... of its V^T operand reads in this tile's V (line_v_tr(lane, p))
+
+  // LDS read bases start at ring stage 0 (tile 0).
+  __device__ __forceinline__ void setup(int lane, float c_, uint32_t ring) {
     li = lane & 31;
     hh = lane >> 5;
-    // K operand (kt, kk): row 32 kt + li, chunk 2 kk + hh of the K line tile
-    // -> k_rd[kk & 3] + 4096 (kk >> 2) + 2048 kt. V^T operand (dt, c4): the
-    // transposed read of the V line tile (tile_io.h), keys in the order of
-    // the P^T B operands.
 #pragma unroll
-    for (int j = 0; j < 4; ++j) k_rd[j] = line_k_rd(lane, j);
-    v_tr[0] = line_v_tr(lane, 0);
-    v_tr[1] = line_v_tr(lane, 1);
+    for (int j = 0; j < 4; ++j) kb4[j] = ring + 2u * (uint32_t)line_k_rd(lane, j);
+    vb2[0] = ring + kVOff + 2u * (uint32_t)line_v_tr(lane, 0);
+    vb2[1] = ring + kVOff + 2u * (uint32_t)line_v_tr(lane, 1);
     c = c_;
     thr_raw = kRescaleThreshold / c;
-  }
-
-  __device__ __forceinline__ void reset() {
+    // Zeros pinned into AGPRs, the file every later MFMA keeps O in.
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) o[dt][r] = 0.f;
-    m_raw = -INFINITY;
+      for (int qb = 0; qb < 2; ++qb) {
+        o[dt][qb] = f32x16{};
+        asm volatile("" : "+a"(o[dt][qb]));
+      }
+    m_raw[0] = m_raw[1] = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) l4[i] = 0.f;
+    for (int qb = 0; qb < 2; ++qb) {
+      lsum[qb] = f32x4{};
+      asm volatile("" : "+a"(lsum[qb]));
+    }
+    // Row sums by v_mfma_f32_16x16x32_bf16 with the P^T operand as B: in that
+    // shape lane l's 8 values are B[k = 8 (l / 16) + i][n = l % 16], i.e.
+    // query n (+16 for odd l / 16) over one half of the chunk's keys. With
+    // A[m][k] = 1 where bit 2 of m equals bit 3 of k, D[m][n] sums query n
+    // for m % 8 < 4 and query n + 16 otherwise, which puts the row sum of
+    // query li = lane % 32 in all four D values of lane `lane`.
+    {
+      const bf16 one = (bf16)(((lane & 15) >> 2 & 1) == ((lane >> 4) & 1) ? 1.0f : 0.0f);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) sel[i] = one;
+      asm volatile("" : "+a"(sel));
+    }
   }
 
-  // Q rows of this wave's 32 queries (qrow0 ..) into its 8 KB of LDS
-  // (tile_io.h row staging); rows past Sq re-read row Sq - 1 (their results
-  // are never stored).
-  __device__ __forceinline__ void dma_q(const FwdParams& p, const Item& it, int qrow0, int lane,
-                                        const bf16* stage) const {
-    stage_rows_in(p.q + it.b * p.qs0 + it.h * p.qs2, p.qs1, qrow0, p.Sq, lane, stage);
-  }
-  // Q^T operands from the staged rows: qreg[kk] = row li, chunk 2 kk + hh.
+  // Q^T operands from this wave's 64 staged rows (two 32-row staging areas),
+  // kept in AGPRs (the MFMA reads its B operand from either file).
   __device__ __forceinline__ void read_q(const bf16* stage, int lane) {
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk) qreg[kk] = staged_operand(stage, lane, kk);
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) {
+        qreg[qb][kk] = staged_operand(stage + qb * 4096, lane, kk);
+        asm volatile("" : "+a"(qreg[qb][kk]));
+      }
   }
 
-  // M block: up to 32 MFMAs in one unrolled stream, fed by a queue of LDS
-  // operands read kPrefetch MFMAs ahead (sched_barrier fences pin the order):
-  //   ops 0-15 : O^T += V^T P^T of the V tile vs, op = 4 c4 + dt (A operand:
-  //              the transposed read of the V rows)
-  //   ops 16-31: S^T = K Q^T of the K tile ks, op = 16 + 2 kk + kt (A operand:
-  //              one 16-byte read of the K tile; two accumulator chains s0, s1)
-  // PV / QK select which half runs (the first tile has no PV, the tail no QK).
-  // A queue of 6 measured about 1% faster than 8, 10 or 12 at every shape
-  // tried (4096x4096, 9216x9216, 4096x512, 1024x1024) and needs fewer VGPRs.
-  template <bool PV, bool QK, int kPrefetch = 6>
-  __device__ __forceinline__ void mblock(const bf16* vs, const bf16* ks) {
-    constexpr int first = PV ? 0 : 16;
-    constexpr int last = QK ? 32 : 16;
-    if constexpr (QK) {
+  // K operand pair j = 8 kb + kk (keys 32 kb .., head-dim 16 kk ..) of the K
+  // tile at kb4.
+  template <int j>
+  __device__ __forceinline__ bf16x8 k_op() const {
+    constexpr int kb = j >> 3, kk = j & 7;
+    return lds_ld16(kb4[kk & 3] + 8192u * (kk >> 2) + 4096u * kb);
+  }
+  // V^T operand pair pp = 4 c4 + dt (d 32 dt .., keys of chunk c4).
+  template <int pp>
+  __device__ __forceinline__ bf16x8 v_op() const {
+    constexpr int c4 = pp >> 2, dt = pp & 3;
+    constexpr uint32_t off = 8192u * (dt >> 1) + 2048u * c4;
+    const s16x4 lo = lds_ld8_tr(vb2[dt & 1] + off);
+    const s16x4 hi = lds_ld8_tr(vb2[dt & 1] + off + 1024u);
+    return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+  }
+  // Moves the K / V^T read bases on by `delta` bytes (the next ring stage).
+  __device__ __forceinline__ void advance_k(uint32_t delta) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        s0[r] = 0.f;
-        s1[r] = 0.f;
-      }
+    for (int j = 0; j < 4; ++j) {
+      kb4[j] += delta;
+      asm volatile("" : "+v"(kb4[j]));
     }
-    bf16x8 q_ops[kPrefetch];
-    auto load_op = [&](int op) -> bf16x8 {
-      if (op < 16) return read_tr_line(vs, op >> 2, op & 3, v_tr[op & 1]);
-      const int kk = (op - 16) >> 1, kt = (op - 16) & 1;
-      return *reinterpret_cast<const bf16x8*>(ks + k_rd[kk & 3] + 4096 * (kk >> 2) + 2048 * kt);
-    };
-    auto run_op = [&](int op, bf16x8 a) {
-      if (op < 16) {
-        const int c4 = op >> 2, dt = op & 3;
-        o[dt] = mfma32(a, pb[c4], o[dt]);
-      } else {
-        const int kk = (op - 16) >> 1, kt = (op - 16) & 1;
-        if (kt == 0) s0 = mfma32(a, qreg[kk], s0);
-        else s1 = mfma32(a, qreg[kk], s1);
-      }
-    };
+  }
+  __device__ __forceinline__ void advance_v(uint32_t delta) {
+    vb2[0] += delta;
+    vb2[1] += delta;
+    asm volatile("" : "+v"(vb2[0]), "+v"(vb2[1]));
+  }
+
+  // Scores of keys at or past klen (tile at key offset kb) to -inf.
+  template <int B>
+  __device__ __forceinline__ void mask(int kb, int klen) {
 #pragma unroll
-    for (int i = first; i < last + kPrefetch; ++i) {
-      // Consume slot (i - first) % kPrefetch before refilling it.
-      if (i - kPrefetch >= first) run_op(i - kPrefetch, q_ops[(i - kPrefetch - first) % kPrefetch]);
-      if (i < last) q_ops[(i - first) % kPrefetch] = load_op(i);
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = kb + 32 * kt + 8 * (r >> 2) + 4 * hh + (r & 3);
+          if (key >= klen) s[B][kt][qb][r] = -INFINITY;
+        }
+  }
+
+  // Max step k (0..15) of S^T buffer B: block kb = k >> 3, query block
+  // qb = k & 1, registers 4 ((k >> 1) & 3) .. + 3, into mx[qb].
+  template <int B, int k>
+  __device__ __forceinline__ void max_step(float (&mx)[2]) const {
+    constexpr int kb = k >> 3, qb = k & 1, r0 = 4 * ((k >> 1) & 3);
+    const f32x16& a = s[B][kb][qb];
+    if constexpr (k < 2) {
+      mx[qb] = max2f(max3f(a[r0], a[r0 + 1], a[r0 + 2]), a[r0 + 3]);
+    } else {
+      mx[qb] = max3f(mx[qb], a[r0], a[r0 + 1]);
+      mx[qb] = max3f(mx[qb], a[r0 + 2], a[r0 + 3]);
+    }
+  }
+
+  // P unit u of S^T buffer B: scores 2 jp, 2 jp + 1 of the P operand (c4, qb),
+  // c4 = u >> 3, qb = (u >> 2) & 1, jp = u & 3, and their sum, in three
+  // stages one slot apart (fma, exp, pack + sum): the stages of consecutive
+  // units share a slot, so no VALU instruction waits on the one before it.
+  // fa / fe carry two units' values between the stages.
+  template <int B, int u>
+  __device__ __forceinline__ void p_fma(const float (&mc)[2], float (&fa)[2][2]) const {
+    constexpr int c4 = u >> 3, qb = (u >> 2) & 1, jp = u & 3;
+    constexpr int kb = c4 >> 1, r = 8 * (c4 & 1) + 2 * jp;
+    fa[u & 1][0] = fmaf(s[B][kb][qb][r], c, -mc[qb]);
+    fa[u & 1][1] = fmaf(s[B][kb][qb][r + 1], c, -mc[qb]);
+    asm volatile("" : "+v"(fa[u & 1][0]), "+v"(fa[u & 1][1]));
+  }
+  template <int u>
+  __device__ __forceinline__ void p_exp(const float (&fa)[2][2], float (&fe)[2][2]) const {
+    fe[u & 1][0] = fast_exp2(fa[u & 1][0]);
+    fe[u & 1][1] = fast_exp2(fa[u & 1][1]);
+    asm volatile("" : "+v"(fe[u & 1][0]), "+v"(fe[u & 1][1]));
+  }
+  template <int u>
+  __device__ __forceinline__ void p_pack(const float (&fe)[2][2]) {
+    constexpr int c4 = u >> 3, qb = (u >> 2) & 1, jp = u & 3;
+    pb[c4][qb][2 * jp] = (bf16)fe[u & 1][0];
+    pb[c4][qb][2 * jp + 1] = (bf16)fe[u & 1][1];
+    // Anchored in its slot: left alone, the compiler sinks the P work next to
+    // its MFMA users.
+    asm volatile("" : "+v"(pb[c4][qb]));
+  }
+  // Row sums of the P operand (c4, qb) on the matrix pipe (see setup): the
+  // VALU alternatives cost the SIMD's vector issue (fp32 adds) or stall the
+  // matrix pipe for half an MFMA each (v_dot2c_f32_bf16).
+  template <int c4, int qb>
+  __device__ __forceinline__ void p_sum() {
+    mfma_rowsum(lsum[qb], sel, pb[c4][qb]);
+  }
+
+  // S^T of the first tile of the range (no other work to interleave).
+  template <int B>
+  __device__ __forceinline__ void qk_first() {
+    bf16x8 kq[kKQ];
+    static_for<0, 32 + 2 * kKPf>([&](auto G) {
+      constexpr int g = decltype(G)::value;
+      static_for<0, 16>([&](auto J) {
+        constexpr int j = decltype(J)::value;
+        if constexpr (kread_slot(j) == g) kq[j % kKQ] = this->template k_op<j>();
+      });
+      if constexpr (g < 32) {
+        constexpr int j = g >> 1, kb = j >> 3, kk = j & 7, qb = g & 1;
+        s[B][kb][qb] = mfma32(kq[j % kKQ], qreg[qb][kk], kk == 0 ? f32x16{} : s[B][kb][qb]);
+      }
       __builtin_amdgcn_sched_barrier(0);
-    }
+    });
   }
 
-  // Softmax of the tile at key offset kb: mask (last tile only), row max,
-  // lazy rescale, P, sums.
-  __device__ __forceinline__ void softmax(int kb, int klen) {
-    const bf16x2 ones = {(bf16)1.0f, (bf16)1.0f};
-    if (kb + kBN > klen) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = kb + 8 * (r >> 2) + 4 * hh + (r & 3);
-        if (key >= klen) s0[r] = -INFINITY;
-        if (key + 32 >= klen) s1[r] = -INFINITY;
+  // Row max of S^T buffer B into mt (no other work).
+  template <int B>
+  __device__ __forceinline__ void max_plain() {
+    float mx[2];
+    static_for<0, 16>([&](auto K) { this->template max_step<B, decltype(K)::value>(mx); });
+    mt[0] = pair_max(mx[0]);
+    mt[1] = pair_max(mx[1]);
+  }
+
+  // One tile t of the slot schedule. S^T of tile t is in buffer SB; with
+  // NEXT, S^T of tile t+1 (its K one ring stage, dstage bytes, past tile t's)
+  // goes to buffer 1 - SB and its row max to mt (masked first when its keys
+  // end inside it: mask_next). The DMA job is issued in its slots.
+  template <int SB, bool NEXT>
+  __device__ __forceinline__ void tile(uint32_t dstage, bool mask_next, int kb_next, int klen,
+                                       const KVDma& dma) {
+    constexpr int NB = 1 - SB;
+    const float mc[2] = {m_raw[0] * c, m_raw[1] * c};
+    if constexpr (NEXT) advance_k(dstage);
+    bf16x8 kq[kKQ], vq[kVQ];
+    float mx[2];
+    float fa[2][2], fe[2][2];
+    static_for<0, 64>([&](auto G) {
+      constexpr int g = decltype(G)::value;
+      if constexpr (NEXT && g == kMaxSlot0) {
+        if (mask_next) mask<NB>(kb_next, klen);
       }
-    }
-    // Row max of the raw scores (two v_max3 chains), then over the lane pair.
-    float ma = max3f(s0[0], s1[0], s0[1]);
-    float mb = max3f(s1[1], s0[2], s1[2]);
-#pragma unroll
-    for (int r = 3; r < 15; r += 2) {
-      ma = max3f(ma, s0[r], s1[r]);
-      mb = max3f(mb, s0[r + 1], s1[r + 1]);
-    }
-    float mt = max3f(ma, mb, max2f(s0[15], s1[15]));
-    mt = pair_max(mt);
-
-    const bool need = mt > m_raw + thr_raw;
-    if (__builtin_amdgcn_ballot_w64(need)) {
-      const float mn = need ? mt : m_raw;
-      const float alpha = fast_exp2((m_raw - mn) * c);
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) l4[i] *= alpha;
-      m_raw = mn;
-    }
-
-    // P^T = exp2(s c - m c) in bf16 as four 16-key B operands.
-    const float mc = m_raw * c;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      pb[0][i] = (bf16)fast_exp2(fmaf(s0[i], c, -mc));
-      pb[1][i] = (bf16)fast_exp2(fmaf(s0[8 + i], c, -mc));
-      pb[2][i] = (bf16)fast_exp2(fmaf(s1[i], c, -mc));
-      pb[3][i] = (bf16)fast_exp2(fmaf(s1[8 + i], c, -mc));
-    }
-    // Row sum of the bf16 P that feeds the MFMA (v_dot2 with ones).
-#pragma unroll
-    for (int c4 = 0; c4 < 4; ++c4) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const bf16x2 pair = {pb[c4][2 * j], pb[c4][2 * j + 1]};
-        l4[c4] = __builtin_amdgcn_fdot2_f32_bf16(pair, ones, l4[c4], false);
+      // Operand reads.
+      if constexpr (NEXT) {
+        static_for<0, 16>([&](auto J) {
+          constexpr int j = decltype(J)::value;
+          if constexpr (kread_slot(j) == g) kq[j % kKQ] = this->template k_op<j>();
+        });
       }
+      static_for<0, 16>([&](auto P) {
+        constexpr int pp = decltype(P)::value;
+        if constexpr (vread_slot(pp) == g) vq[pp % kVQ] = this->template v_op<pp>();
+      });
+      // The slot's MFMA.
+      if constexpr (g < 32) {
+        if constexpr (NEXT) {
+          constexpr int j = g >> 1, kb = j >> 3, kk = j & 7, qb = g & 1;
+          s[NB][kb][qb] = mfma32(kq[j % kKQ], qreg[qb][kk], kk == 0 ? f32x16{} : s[NB][kb][qb]);
+        }
+      } else {
+        constexpr int op = g - 32, pp = op >> 1, c4 = pp >> 2, dt = pp & 3, qb = op & 1;
+        mfma_pv(o[dt][qb], vq[pp % kVQ], pb[c4][qb]);
+        if constexpr (dt == 2) this->template p_sum<c4, qb>();
+      }
+
+      // P units of tile t, three stages per unit.
+      static_for<0, 32>([&](auto U) {
+        constexpr int u = decltype(U)::value;
+        if constexpr (exp_slot(u) == g) this->template p_fma<SB, u>(mc, fa);
+        if constexpr (exp_slot(u) + 1 == g) this->template p_exp<u>(fa, fe);
+        if constexpr (exp_slot(u) + 2 == g) this->template p_pack<u>(fe);
+      });
+      // Row max of tile t+1.
+      if constexpr (NEXT && g >= kMaxSlot0) {
+        this->template max_step<NB, g - kMaxSlot0>(mx);
+        asm volatile("" : "+v"(mx[0]), "+v"(mx[1]));
+      }
+      // DMA.
+      static_for<0, 8>([&](auto I) {
+        constexpr int i = decltype(I)::value;
+        if constexpr (dma_slot(i) == g) dma.template issue<i>();
+      });
+      // The operands of the previous slot's inline-asm MFMA stay allocated to
+      // the end of this slot: the compiler does not see that MFMA still
+      // reading them and would hand their registers to this slot's VALU
+      // results, whose writes would then wait for it.
+      if constexpr (g > 32) {
+        constexpr int op = g - 33, pp = op >> 1, c4 = pp >> 2, dt = pp & 3, qb = op & 1;
+        keep_alive(vq[pp % kVQ]);
+        if constexpr (dt == 3) keep_alive(pb[c4][qb]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    keep_alive(vq[15 % kVQ]);
+    keep_alive(pb[3][1]);
+    advance_v(dstage);
+    if constexpr (NEXT) {
+      mt[0] = pair_max(mx[0]);
+      mt[1] = pair_max(mx[1]);
     }
   }
 
-  // Partial result of one key range: O / l rounded to bf16 and the range's
-  // LSE (fp32), for the combine pass (no padding correction here). `row` is
-  // the (item, split) record; the wave holds queries qloc0 .. qloc0 + 31. The
-  // rows leave like O in the epilogue (row staging, 4 whole 256-byte rows per
-  // store). In fp32 the partials doubled the bytes a short forward writes and
-  // its combine pass reads (config 1: 33.8 MB).
-  __device__ __forceinline__ void store_partial(const FwdParams& p, int64_t row, int qloc0,
-                                                int lane, bf16* stage) const {
-    const float l_tot = pair_sum((l4[0] + l4[1]) + (l4[2] + l4[3]));
-    const bool any = l_tot > 0.f;
-    const float lse = any ? (m_raw * c + __log2f(l_tot)) * kLn2 : -INFINITY;
-    const float scale = any ? 1.0f / l_tot : 0.f;
-    stage_acc_rows(o, scale, lane, stage);
-    stage_rows_out(p.part_o + row * kQPerWg * kD, kD, qloc0, kQPerWg, lane, stage);
-    if (hh == 0) p.part_lse[row * kQPerWg + qloc0 + li] = lse;
+  // Keeps O in AGPRs up to this point and orders the VALU code that follows
+  // after every MFMA that wrote it.
+  __device__ __forceinline__ void fence_o() {
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3"
+                 : "+a"(o[0][0]), "+a"(o[1][0]), "+a"(o[2][0]), "+a"(o[3][0]), "+a"(o[0][1]),
+                   "+a"(o[1][1]), "+a"(o[2][1]), "+a"(o[3][1]), "+a"(lsum[0]), "+a"(lsum[1]));
   }
 
-  // Normalise, optional padding correction, store O and LSE of queries
-  // qrow0 .. qrow0 + 31. O goes out through this wave's 8 KB of LDS (tile_io.h
-  // row staging), 4 whole 256-byte rows per store.
-  __device__ __forceinline__ void epilogue(const FwdParams& p, const Item& it, int qrow0, int lane,
-                                           bf16* stage) const {
-    const int qrow = qrow0 + li;
-    const float m_run = m_raw * c;
-    const float l_run = (l4[0] + l4[1]) + (l4[2] + l4[3]);
-    const float l_tot = pair_sum(l_run);
+  // Lazy rescale for the next tile's max mt: m is raised (and O and l scaled
+  // down) only where mt exceeds it by more than thr_raw.
+  __device__ __forceinline__ void update_max() {
+    const bool n0 = mt[0] > m_raw[0] + thr_raw;
+    const bool n1 = mt[1] > m_raw[1] + thr_raw;
+    if (__builtin_amdgcn_ballot_w64(n0 || n1)) {
+      const float mn0 = n0 ? mt[0] : m_raw[0];
+      const float mn1 = n1 ? mt[1] : m_raw[1];
+      const float a0 = fast_exp2((m_raw[0] - mn0) * c);
+      const float a1 = fast_exp2((m_raw[1] - mn1) * c);
+      fence_o();
+      // One accumulator block at a time, pinned back into AGPRs: otherwise the
+      // compiler reads all 128 values into VGPRs first.
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[dt][0][r] *= a0;
+        asm volatile("" : "+a"(o[dt][0]));
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[dt][1][r] *= a1;
+        asm volatile("" : "+a"(o[dt][1]));
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        lsum[0][r] *= a0;
+        lsum[1][r] *= a1;
+      }
+      asm volatile("" : "+a"(lsum[0]), "+a"(lsum[1]));
+      m_raw[0] = mn0;
+      m_raw[1] = mn1;
+    }
+  }
+
+  // O (or the range's partial O) of query block qb: O / l, optional padding
+  // correction, bf16, out through the 8 KB staging area `stage` (tile_io.h
+  // row staging, 4 whole 256-byte rows per store); LSE in fp32.
+  template <int qb>
+  __device__ __forceinline__ float finish(float pad_ln, bool pad, bf16* obase, int64_t ors,
+                                          int orow0, int onrows, int lane, bf16* stage) const {
+    const float l_tot = lsum[qb][0];
     const bool any = l_tot > 0.f;
-    const float lse = any ? (m_run + __log2f(l_tot)) * kLn2 : -INFINITY;
+    const float lse = any ? (m_raw[qb] * c + __log2f(l_tot)) * kLn2 : -INFINITY;
     float scale = any ? 1.0f / l_tot : 0.f;
-    if (p.ln_pad) scale *= 1.0f / (1.0f + expf(p.ln_pad[it.b] - lse));
-    stage_acc_rows(o, scale, lane, stage);
-    if (p.lse && hh == 0 && qrow < p.Sq) p.lse[((int64_t)it.b * p.H + it.h) * p.Sq + qrow] = lse;
-    stage_rows_out(p.o + it.b * p.os0 + it.h * p.os2, p.os1, qrow0, p.Sq, lane, stage);
+    if (pad) scale *= 1.0f / (1.0f + expf(pad_ln - lse));
+    const f32x16 ob[4] = {o[0][qb], o[1][qb], o[2][qb], o[3][qb]};
+    stage_acc_rows(ob, scale, lane, stage);
+    stage_rows_out(obase, ors, orow0, onrows, lane, stage);
+    return lse;
   }
 };
 
-// Phase-shifted ("ping-pong") schedule. Waves 0-3 (group A) and 4-7 (group B)
-// run the same per-tile work, one phase apart:
-//   M(j): O^T += V_{j-1}^T P_{j-1}^T (16 MFMA) and S_j^T = K_j Q^T (16 MFMA)
-//   X(j): softmax of S_j -> P_j (exp, max, sums, rare rescale)
-//   phase 2j  : A runs M(j), B runs X(j-1)
-//   phase 2j+1: A runs X(j), B runs M(j)
-// with a workgroup barrier between phases. Waves w and w+4 share a SIMD, so
-// on every SIMD one wave is in an MFMA block while its partner is in a VALU
-// block and the matrix and vector pipes overlap. Tile j sits in stage
-// j % kStages; its DMA is issued at phase 2(j-kAhead)+1 and complete (wait +
-// barrier) by the end of phase 2j-1; its K is read in phases 2j, 2j+1 and
-// its V in 2j+2, 2j+3. Both groups run the same instruction stream,
-// M(m) | barrier | X(m) | barrier; group B executes one extra barrier first
-// (group A one extra at the end), which shifts B by exactly one phase. Only
-// group A issues and waits for the DMA: tile m+kAhead at the start of its
-// X(m), off the MFMA stream (the stage it overwrites held tile m-2, whose V
-// group B last read in phase 2m-1), and tile m+1 is complete before the
-// barrier that ends its X(m); the barriers order it for group B.
-//
-// One workgroup per work item (256 queries of one (batch, head)), or per
-// key range of one of the last work items when they are split.
-__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
+// One workgroup per work item (256 queries of one (batch, head)), or per key
+// range of one of the last work items when they are split.
+__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void attn_fwd_kernel(FwdParams p) {
-  __shared__ __attribute__((aligned(1024))) bf16 kv_lds[kStages][2][kTileElems];
+  __shared__ __attribute__((aligned(1024))) bf16 kv_lds[kStages * 2 * kTileElems];
 
   // Block -> work item. Blocks start in index order, so block r * R + j
   // (R = round_blocks) runs in round r: it takes an item of that round's
@@ -427,64 +592,116 @@ void attn_fwd_kernel(FwdParams p) {
   }
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const bool group_a = wave < 4;
   const int lane = tid & 63;
-  const int qloc = wave * 32 + (lane & 31);
-  const int qrow = it.qblk * kQPerWg + qloc;
+  const int qrow0 = it.qblk * kQPerWg + wave * kQPerWave;  // the wave's first query
+
+  const uint32_t ring = lds_addr(kv_lds);
+  auto stage_addr = [&](int t) -> uint32_t { return ring + (uint32_t)(t % kStages) * kStageBytes; };
 
   FwdWave w;
-  w.setup(lane, p.c);
-  // Q rows staged in ring stages 2 and 3 (free until tile 2's DMA, which
-  // group A issues after the first barrier that follows every wave's read).
-  bf16* qstage = &kv_lds[2 + (wave >> 2)][0][0] + (wave & 3) * 4096;
-  w.dma_q(p, it, qrow - (lane & 31), lane, qstage);
-  w.reset();
+  w.setup(lane, p.c, ring);
+  // Q rows staged in ring stages 2 and 3 (16 KB per wave), free until tile
+  // 2's DMA, which is issued after the barrier that follows every wave's read.
+  bf16* qstage = kv_lds + 2 * (2 * kTileElems) + wave * 8192;
+  {
+    const bf16* qb = p.q + it.b * p.qs0 + it.h * p.qs2;
+    stage_rows_in(qb, p.qs1, qrow0, p.Sq, lane, qstage);
+    stage_rows_in(qb, p.qs1, qrow0 + 32, p.Sq, lane, qstage + 4096);
+  }
   KVDma dma;
   dma.setup(p, wave, lane);
   const bf16* kp = p.k + it.b * p.ks0 + it.h * p.ks2;
   const bf16* vp = p.v + it.b * p.vs0 + it.h * p.vs2;
-  auto issue_tile = [&](int t) {
-    dma.issue(p, kp, vp, it.klen, t0 + t, kv_lds[t % kStages][0], kv_lds[t % kStages][1]);
+  auto issue_job = [&](int t) {  // the whole job of tile t at once
+    dma.prepare(p, t < ntiles, (t0 + t) * kBN, stage_addr(t), wave, kp, vp, lane);
+    static_for<0, 8>([&](auto I) { dma.template issue<decltype(I)::value>(); });
   };
-
-  static_assert(kAhead >= 1 && kAhead <= 4, "lookahead");
-  auto wait_for_next = [&](int m) {  // tile m+1 complete; later issued tiles may be in flight
-    const int last_issued = min(m + kAhead, ntiles - 1);
-    wait_dma_tiles_in_flight(max(last_issued - (m + 1), 0));
-  };
-  if (group_a && ntiles > 0) {
-    for (int t = 0; t < kAhead && t < ntiles; ++t) issue_tile(t);
-    wait_for_next(-1);  // also the Q rows, issued before
-  } else {
-    wait_dma();
-  }
-  w.read_q(qstage, lane);
-  __syncthreads();
-  if (!group_a) __syncthreads();
   if (ntiles > 0) {
-    w.mblock<false, true>(kv_lds[0][1], kv_lds[0][0]);
-    __syncthreads();
-    if (group_a && kAhead < ntiles) issue_tile(kAhead);
-    w.softmax(t0 * kBN, it.klen);
-    if (group_a) wait_for_next(0);
-    __syncthreads();
-    for (int m = 1; m < ntiles; ++m) {
-      w.mblock<true, true>(kv_lds[(m - 1) % kStages][1], kv_lds[m % kStages][0]);
-      __syncthreads();
-      if (group_a && m + kAhead < ntiles) issue_tile(m + kAhead);
-      w.softmax((t0 + m) * kBN, it.klen);
-      if (group_a) wait_for_next(m);
-      __syncthreads();
-    }
-    w.mblock<true, false>(kv_lds[(ntiles - 1) % kStages][1], kv_lds[0][0]);
+    issue_job(0);
+    issue_job(1);
   }
-  if (group_a) __syncthreads();
-  // Output staging: the two stages after the last tile's are free (group B
-  // may still be reading the last tile's V in its final M block; nothing else
-  // is read or in flight).
-  bf16* stage = &kv_lds[(ntiles + (wave >> 2)) % kStages][0][0] + (wave & 3) * 4096;
-  if (split < 0) w.epilogue(p, it, qrow - (lane & 31), lane, stage);
-  else w.store_partial(p, (int64_t)(item_idx - p.full_blocks) * p.nsplit + split, wave * 32, lane, stage);
+  wait_dma();
+  __syncthreads();  // tiles 0 and 1 from every wave
+  w.read_q(qstage, lane);
+  __syncthreads();  // every wave has read its Q rows
+  if (ntiles > 0) {
+    issue_job(2);
+    // S^T of tile t lives in buffer (b0 + t) & 1, with b0 chosen so that the
+    // last tile, the one without a next tile, always uses buffer 0.
+    const int b0 = (ntiles - 1) & 1;
+    const int kb0 = t0 * kBN;
+    if (b0) {
+      w.qk_first<1>();
+      if (kb0 + kBN > it.klen) w.mask<1>(kb0, it.klen);
+      w.max_plain<1>();
+    } else {
+      w.qk_first<0>();
+      if (kb0 + kBN > it.klen) w.mask<0>(kb0, it.klen);
+      w.max_plain<0>();
+    }
+    w.m_raw[0] = w.mt[0];
+    w.m_raw[1] = w.mt[1];
+
+    // Tile t: at its top, tile t+1 (issued two tiles earlier) is complete in
+    // this wave (at most the job of tile t+2 is in flight) and the barrier
+    // publishes every wave's part. The job issued during tile t, tile t+3,
+    // reuses the stage of tile t-1, whose K was read in tile t-2 and V in
+    // tile t-1, before that barrier.
+    auto top = [&](int t) {
+      asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+      __syncthreads();
+      const int tn = t + kLead;
+      dma.prepare(p, tn < ntiles, (t0 + tn) * kBN, stage_addr(tn), wave, kp, vp, lane);
+    };
+    auto run = [&](auto sb, auto next, int t) {
+      constexpr int SB = decltype(sb)::value;
+      constexpr bool NEXT = decltype(next)::value;
+      top(t);
+      const int kbn = (t0 + t + 1) * kBN;
+      w.tile<SB, NEXT>(stage_addr(t + 1) - stage_addr(t), kbn + kBN > it.klen, kbn, it.klen, dma);
+      if constexpr (NEXT) w.update_max();
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    int t = 0;
+    if (b0) {
+      run(I1{}, std::true_type{}, 0);
+      t = 1;
+    }
+    for (; t + 1 < ntiles; t += 2) {
+      run(I0{}, std::true_type{}, t);
+      run(I1{}, std::true_type{}, t + 1);
+    }
+    run(I0{}, std::false_type{}, t);  // t == ntiles - 1
+  }
+  wait_dma();
+  __syncthreads();  // every wave is done with the ring; no DMA in flight
+
+  // Output through the ring: 16 KB per wave.
+  w.fence_o();
+  bf16* stage = kv_lds + wave * 8192;
+  if (split < 0) {
+    const bool pad = p.ln_pad != nullptr;
+    const float pad_ln = pad ? p.ln_pad[it.b] : 0.f;
+    bf16* obase = p.o + it.b * p.os0 + it.h * p.os2;
+    const float lse0 = w.finish<0>(pad_ln, pad, obase, p.os1, qrow0, p.Sq, lane, stage);
+    const float lse1 = w.finish<1>(pad_ln, pad, obase, p.os1, qrow0 + 32, p.Sq, lane, stage + 4096);
+    if (p.lse && w.hh == 0) {
+      float* lp = p.lse + ((int64_t)it.b * p.H + it.h) * p.Sq;
+      if (qrow0 + w.li < p.Sq) lp[qrow0 + w.li] = lse0;
+      if (qrow0 + 32 + w.li < p.Sq) lp[qrow0 + 32 + w.li] = lse1;
+    }
+  } else {
+    const int64_t row = (int64_t)(item_idx - p.full_blocks) * p.nsplit + split;
+    bf16* obase = p.part_o + row * kQPerWg * kD;
+    const int q0 = wave * kQPerWave;
+    const float lse0 = w.finish<0>(0.f, false, obase, kD, q0, kQPerWg, lane, stage);
+    const float lse1 = w.finish<1>(0.f, false, obase, kD, q0 + 32, kQPerWg, lane, stage + 4096);
+    if (w.hh == 0) {
+      p.part_lse[row * kQPerWg + q0 + w.li] = lse0;
+      p.part_lse[row * kQPerWg + q0 + 32 + w.li] = lse1;
+    }
+  }
 }
 
 // Merges the key-range partials of the split work items: 16 queries per
@@ -599,7 +816,9 @@ static int prepare(const aa_attn_fwd_args* a, FwdParams& p) {
   if (a->Sq > (1 << 30) || a->Sk > (1 << 30) || a->H > 65535 || a->B > 65535)
     return fail(AA_EUNSUPPORTED, "attn_fwd: size out of range");
   if (a->B == 0 || a->Sq == 0) return AA_OK;
-  if (!a->q || !a->k || !a->v || !a->out) return fail(AA_EINVAL, "attn_fwd: null tensor");
+  // K and V may be null when there are no keys (nothing reads them).
+  if (!a->q || !a->out || (a->Sk > 0 && (!a->k || !a->v)))
+    return fail(AA_EINVAL, "attn_fwd: null tensor");
   if (!aligned16(a->q) || !aligned16(a->k) || !aligned16(a->v) || !aligned16(a->out))
     return fail(AA_EINVAL, "attn_fwd: tensors must be 16-byte aligned");
   if (!stride_ok(a->q_stride) || !stride_ok(a->k_stride) || !stride_ok(a->v_stride) ||

@@ -10,8 +10,8 @@
 //   32 d x 32 queries, 192 registers) stay in registers for the whole range,
 //   which takes the whole register file of a SIMD, hence one wave per SIMD.
 //   With B * H * S / 128 work items short of the CU count (128 items at
-//   16384 tokens), the keys are split into ranges whose normalised fp32
-//   partials attn_fwd_d384_combine_kernel merges.
+//   16384 tokens), the keys are split into ranges whose normalised partials
+//   (bf16 O, fp32 LSE) attn_fwd_d384_combine_kernel merges.
 //
 // Per 32-key tile and wave: S^T = K Q^T is one 32x32 accumulator, 24
 //   v_mfma_f32_32x32x16_bf16 over the head dimension (A = 16-byte reads of
@@ -79,14 +79,6 @@ struct Params {
   bf16* part_o;     // [items * nsplit][128][384] normalised partials, bf16
   float* part_lse;  // [items * nsplit][128]
 };
-
-template <int B, int E, typename F>
-__device__ __forceinline__ void static_for(F&& f) {
-  if constexpr (B < E) {
-    f(std::integral_constant<int, B>{});
-    static_for<B + 1, E>(f);
-  }
-}
 
 // DMA blocks 4 g .. 4 g + 3 of a row tile (not swizzled) whose row 0 is at
 // `base`: rows 16 g + (lane & 15), chunk 4 i + lq (lq = lane >> 4) for block
@@ -542,7 +534,7 @@ __global__ __launch_bounds__(192) void attn_fwd_d384_combine_kernel(Params p) {
 
 // Key split: ranges per work item so that items x ranges fills the CUs
 // without exceeding them (one round), at most 8, each of at least 4 tiles.
-// items x ranges <= ncu bounds the partials at ncu x 128 x 385 floats.
+// items x ranges <= ncu bounds the partials at ncu x 128 x (384 bf16 + 1 float).
 static int plan_split(int64_t items, int64_t Sk, int ncu) {
   if (items <= 0 || ncu <= 0 || 2 * items > ncu) return 1;
   const int64_t tiles = (Sk + kBN - 1) / kBN;
@@ -575,8 +567,10 @@ int attn_fwd_d384(const aa_attn_fwd_args* a, int ncu, hipStream_t stream) {
   using namespace d384;
   if (a->B < 0 || a->Sq < 0 || a->Sk < 0 || a->H <= 0) return fail(AA_EINVAL, "attn_fwd: negative size");
   if (a->B == 0 || a->Sq == 0) return AA_OK;
-  if (a->Sk == 0) return fail(AA_EINVAL, "attn_fwd: Sk must be >= 1 at head_dim 384");
-  if (!a->q || !a->k || !a->v || !a->out) return fail(AA_EINVAL, "attn_fwd: null tensor");
+  // Sk == 0 is accepted as at head_dim 128: every work item has an empty key
+  // range, reads no K/V and writes O = 0, LSE = -inf.
+  if (!a->q || !a->out || (a->Sk > 0 && (!a->k || !a->v)))
+    return fail(AA_EINVAL, "attn_fwd: null tensor");
   if (a->ln_pad && !a->seqused_k) return fail(AA_EINVAL, "attn_fwd: ln_pad needs seqused_k");
   if (!(a->softmax_scale > 0.f) || !std::isfinite(a->softmax_scale))
     return fail(AA_EINVAL, "attn_fwd: softmax_scale must be positive and finite");

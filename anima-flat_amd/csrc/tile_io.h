@@ -135,10 +135,10 @@ __device__ __forceinline__ s16x4 lds_ld8_tr(uint32_t addr) {
 //     pieces cover all 64 banks.
 
 // DMA of 16 bytes per lane from sbase + voff (sbase wave-uniform, held in
-// SGPRs: the per-lane address is one 32-bit byte offset) to LDS at
-// lds_dst + 16 lane.
-__device__ __forceinline__ void dma16_sv(const void* sbase, uint32_t voff, const void* lds_dst) {
-  const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void*)lds_dst);
+// SGPRs: the per-lane address is one 32-bit byte offset) to LDS at byte
+// address lds_byte + 16 lane.
+__device__ __forceinline__ void dma16_sva(const void* sbase, uint32_t voff, uint32_t lds_byte) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_byte);
   // readfirstlane returns int: widen each half through uint32_t (a signed
   // int would sign-extend the low half into the high one).
   const uint64_t sb = (uint64_t)(uintptr_t)sbase;
@@ -147,6 +147,10 @@ __device__ __forceinline__ void dma16_sv(const void* sbase, uint32_t voff, const
   const uint64_t sbu = ((uint64_t)hi << 32) | (uint64_t)lo;
   asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbu), "s"(m0)
                : "memory", "m0");
+}
+// The same with the LDS destination as a pointer into __shared__ memory.
+__device__ __forceinline__ void dma16_sv(const void* sbase, uint32_t voff, const void* lds_dst) {
+  dma16_sva(sbase, voff, (uint32_t)(uintptr_t)(lds_void*)lds_dst);
 }
 
 // Chunk (0..7, within the block's 64 d) that DMA lane `lane` moves into its

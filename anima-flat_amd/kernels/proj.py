@@ -36,29 +36,17 @@ def _qkv_proj_norm_rope(
     q = hid.new_empty((B, S, heads, hd))
     k = torch.empty_like(q)
     v = torch.empty_like(q)
+    qw, kw, c32, s32 = _f32(q_weight), _f32(k_weight), _f32(cos), _f32(sin)
     with torch.cuda.device(hid.device):
-        _lib.check(
-            _lib.lib().aa_qkv_proj_norm_rope(
-                hid.data_ptr(),
-                hid.stride(1),
-                weight.data_ptr(),
-                q.data_ptr(),
-                k.data_ptr(),
-                v.data_ptr(),
-                _f32(q_weight).data_ptr(),
-                _f32(k_weight).data_ptr(),
-                _f32(cos).data_ptr(),
-                _f32(sin).data_ptr(),
-                B,
-                S,
-                heads,
-                hd,
-                eps,
-                _lib.dtype_code(hid),
-                _lib.stream(hid),
-            ),
-            "qkv_proj_norm_rope",
-        )
+        for sl, rows, rs in _row_launches(hid):
+            _lib.check(
+                _lib.lib().aa_qkv_proj_norm_rope(
+                    rows.data_ptr(), rs, weight.data_ptr(), q[sl].data_ptr(), k[sl].data_ptr(),
+                    v[sl].data_ptr(), qw.data_ptr(), kw.data_ptr(), c32.data_ptr(), s32.data_ptr(),
+                    rows.shape[0], S, heads, hd, eps, _lib.dtype_code(hid), _lib.stream(hid),
+                ),
+                "qkv_proj_norm_rope",
+            )
     return q, k, v
 
 
@@ -75,7 +63,8 @@ def qkv_proj_norm_rope(hid, weight, q_weight, k_weight, cos, sin, heads, eps=1e-
     projection output kept on chip. Inference only (no autograd).
 
     Args:
-        hid: `[B, S, heads * head_dim]` bf16; rows may be strided (last-dim stride 1).
+        hid: `[B, S, heads * head_dim]` bf16, last-dim stride 1; rows and batch items may
+            be strided.
         weight: `[3 * heads * head_dim, heads * head_dim]` bf16, contiguous (nn.Linear, no bias).
         q_weight, k_weight, cos, sin, heads, eps: as for `qkv_norm_rope`.
 
@@ -85,8 +74,8 @@ def qkv_proj_norm_rope(hid, weight, q_weight, k_weight, cos, sin, heads, eps=1e-
     _check(hid, weight, q_weight, k_weight, cos, sin)
     hd = 2 * cos.shape[1]
     D = heads * hd
-    if hid.ndim != 3 or hid.shape[-1] != D or hid.stride(-1) != 1 or hid.stride(0) != hid.shape[1] * hid.stride(1):
-        raise ValueError("hid must be [B, S, heads * head_dim] with unit last-dim stride and uniform rows")
+    if not _rows_ok(hid) or hid.shape[-1] != D:
+        raise ValueError("hid must be [B, S, heads * head_dim] with unit last-dim stride")
     if not weight.is_contiguous() or tuple(weight.shape) != (3 * D, D) or weight.dtype != hid.dtype:
         raise ValueError("weight must be a contiguous [3 * heads * head_dim, heads * head_dim] matrix of hid's dtype")
     if cos.shape != sin.shape or cos.shape[0] != hid.shape[1] or (cos.shape[1] & (cos.shape[1] - 1)):
@@ -100,8 +89,26 @@ def qkv_proj_norm_rope(hid, weight, q_weight, k_weight, cos, sin, heads, eps=1e-
 
 
 def _rows_ok(x: torch.Tensor) -> bool:
-    """[B, S, K] with unit last-dim stride and uniform rows (one row stride)."""
-    return x.ndim == 3 and x.stride(-1) == 1 and x.stride(0) == x.shape[1] * x.stride(1)
+    """[B, S, K] with unit last-dim stride (any batch and row strides)."""
+    return x.ndim == 3 and x.stride(-1) == 1
+
+
+def _row_launches(x: torch.Tensor):
+    """How to hand the rows of a [B, S, K] input to the C ABI, which addresses
+    them as B * S rows at one row stride: a list of (batch slice, rows view,
+    row stride). One launch when the rows are uniform (always so for B == 1:
+    the batch stride then addresses nothing); otherwise one per batch item,
+    each item's S rows being uniform. A sequence-trimmed view such as
+    `ctx[:, :keep]` (src/model.py:251) has stride(0) = S_full * K, not keep * K.
+    """
+    B, S, K = x.shape
+    if S == 1:
+        if B == 1 or x.stride(0) >= K:
+            return [(slice(None), x, x.stride(0) if B > 1 else K)]
+        return [(slice(b, b + 1), x[b : b + 1], K) for b in range(B)]
+    if B == 1 or x.stride(0) == S * x.stride(1):
+        return [(slice(None), x, x.stride(1))]
+    return [(slice(b, b + 1), x[b : b + 1], x.stride(1)) for b in range(B)]
 
 
 @custom_op("anima_flat_amd::proj_head_norm", mutates_args=())
@@ -111,15 +118,16 @@ def _proj_head_norm(
     B, S, K = x.shape
     hd = norm_weight.numel()
     y = x.new_empty((B, S, heads, hd))
+    nw = _f32(norm_weight)
     with torch.cuda.device(x.device):
-        _lib.check(
-            _lib.lib().aa_proj_head_norm(
-                x.data_ptr(), x.stride(1), weight.data_ptr(), K, y.data_ptr(),
-                _f32(norm_weight).data_ptr(), B, S, heads, hd, eps, _lib.dtype_code(x),
-                _lib.stream(x),
-            ),
-            "proj_head_norm",
-        )
+        for sl, rows, rs in _row_launches(x):
+            _lib.check(
+                _lib.lib().aa_proj_head_norm(
+                    rows.data_ptr(), rs, weight.data_ptr(), K, y[sl].data_ptr(), nw.data_ptr(),
+                    rows.shape[0], S, heads, hd, eps, _lib.dtype_code(x), _lib.stream(x),
+                ),
+                "proj_head_norm",
+            )
     return y
 
 
@@ -136,7 +144,8 @@ def proj_head_norm(x, weight, norm_weight, heads, eps=1e-5):
     the projection output kept on chip. Inference only (no autograd).
 
     Args:
-        x: `[B, S, K]` bf16 (K a multiple of 32); rows may be strided (last-dim stride 1).
+        x: `[B, S, K]` bf16 (K a multiple of 32), last-dim stride 1; rows and batch items
+            may be strided.
         weight: `[heads * head_dim, K]` bf16, contiguous (nn.Linear, no bias).
         norm_weight: RMSNorm weight `[head_dim]`.
         heads, eps: as for `head_norm`.
@@ -148,7 +157,7 @@ def proj_head_norm(x, weight, norm_weight, heads, eps=1e-5):
     hd = norm_weight.numel()
     _check_hd(hd)
     if not _rows_ok(x):
-        raise ValueError("x must be [B, S, K] with unit last-dim stride and uniform rows")
+        raise ValueError("x must be [B, S, K] with unit last-dim stride")
     if not weight.is_contiguous() or tuple(weight.shape) != (heads * hd, x.shape[-1]) or weight.dtype != x.dtype:
         raise ValueError("weight must be a contiguous [heads * head_dim, K] matrix of x's dtype")
     if torch.is_grad_enabled() and (x.requires_grad or weight.requires_grad or norm_weight.requires_grad):
@@ -164,15 +173,17 @@ def _kv_proj_norm(
     hd = k_weight.numel()
     k = ctx.new_empty((B, S, heads, hd))
     v = torch.empty_like(k)
+    kw = _f32(k_weight)
     with torch.cuda.device(ctx.device):
-        _lib.check(
-            _lib.lib().aa_kv_proj_norm(
-                ctx.data_ptr(), ctx.stride(1), weight.data_ptr(), K, k.data_ptr(), v.data_ptr(),
-                _f32(k_weight).data_ptr(), B, S, heads, hd, eps, _lib.dtype_code(ctx),
-                _lib.stream(ctx),
-            ),
-            "kv_proj_norm",
-        )
+        for sl, rows, rs in _row_launches(ctx):
+            _lib.check(
+                _lib.lib().aa_kv_proj_norm(
+                    rows.data_ptr(), rs, weight.data_ptr(), K, k[sl].data_ptr(), v[sl].data_ptr(),
+                    kw.data_ptr(), rows.shape[0], S, heads, hd, eps, _lib.dtype_code(ctx),
+                    _lib.stream(ctx),
+                ),
+                "kv_proj_norm",
+            )
     return k, v
 
 
@@ -191,8 +202,9 @@ def kv_proj_norm(ctx, weight, k_weight, heads, eps=1e-5):
     projection output kept on chip. Inference only (no autograd).
 
     Args:
-        ctx: `[B, S, K]` bf16 text context (K = text_dim, a multiple of 32); rows may
-            be strided (last-dim stride 1).
+        ctx: `[B, S, K]` bf16 text context (K = text_dim, a multiple of 32), last-dim
+            stride 1; rows and batch items may be strided, e.g. the sequence-trimmed
+            `ctx[:, :keep]` of `trim_context` (src/model.py:248-253).
         weight: `[2 * heads * head_dim, K]` bf16, contiguous (nn.Linear, no bias).
         k_weight: RMSNorm weight `[head_dim]`; applied in the activation dtype as
             F.rms_norm does, so pass `b.xk_norm.to(ctx.dtype)` as the reference does.
@@ -205,7 +217,7 @@ def kv_proj_norm(ctx, weight, k_weight, heads, eps=1e-5):
     hd = k_weight.numel()
     _check_hd(hd)
     if not _rows_ok(ctx):
-        raise ValueError("ctx must be [B, S, K] with unit last-dim stride and uniform rows")
+        raise ValueError("ctx must be [B, S, K] with unit last-dim stride")
     if not weight.is_contiguous() or tuple(weight.shape) != (2 * heads * hd, ctx.shape[-1]) or weight.dtype != ctx.dtype:
         raise ValueError("weight must be a contiguous [2 * heads * head_dim, K] matrix of ctx's dtype")
     if torch.is_grad_enabled() and (ctx.requires_grad or weight.requires_grad or k_weight.requires_grad):

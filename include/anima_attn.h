@@ -178,9 +178,9 @@ int aa_head_norm_bwd(const void* x, const void* dy, void* dx,
 
 typedef struct aa_attn_fwd_args {
   const void* q;        /* [B, Sq, H, hd] */
-  const void* k;        /* [B, Sk, H, hd] */
-  const void* v;        /* [B, Sk, H, hd] */
-  void* out;            /* [B, Sq, H, hd] */
+  const void* k;        /* [B, Sk, H, hd]; may be NULL when Sk == 0 */
+  const void* v;        /* [B, Sk, H, hd]; may be NULL when Sk == 0 */
+  void* out;            /* [B, Sq, H, hd]; Sk == 0 gives out = 0 and lse = -inf */
   float* lse;           /* [B, H, Sq] contiguous natural-log LSE, or NULL */
   const int32_t* seqused_k; /* [B] keys attended per batch item, or NULL (all Sk) */
   const float* ln_pad;  /* [B] log(#padding keys) for the fused padding
@@ -197,7 +197,7 @@ typedef struct aa_attn_fwd_args {
 } aa_attn_fwd_args;
 
 /* Bytes of device workspace aa_attn_fwd needs on the current device: partial
- * results (hd 128: bf16 O and fp32 LSE; hd 384: fp32) when the work items (256
+ * results (bf16 normalised O and fp32 LSE, at both head dims) when the work items (256
  * queries of one (batch, head); 128 at hd 384) of a partial last round of
  * workgroups (at hd 384: of too few work items to fill the device) are split
  * over key ranges, else 0. */

@@ -290,6 +290,31 @@ def test_trim_context_bookkeeping(pkg):
     assert t2.shape[1] == 8 and s2.tolist() == [8] and math.isinf(l2.item()) and l2.item() < 0
 
 
+def test_projection_row_launches(proj):
+    """The fused projections hand B * S input rows to the C ABI at one row
+    stride: uniform rows go in one launch (for B == 1 whatever the batch
+    stride), a sequence-trimmed context view (src/model.py:251) in one launch
+    per batch item, each item's rows at the view's row stride."""
+    plan = proj._row_launches
+    x = torch.zeros(2, 512, 1024)
+    (only,) = plan(x)
+    assert only[0] == slice(None) and only[2] == 1024
+    trimmed = x[:, :328]
+    launches = plan(trimmed)
+    assert len(launches) == 2 and all(rs == 1024 for _, _, rs in launches)
+    for b, (sl, rows, _) in enumerate(launches):
+        assert sl == slice(b, b + 1) and rows.shape == (1, 328, 1024)
+        assert rows.data_ptr() == trimmed[b].data_ptr()
+    (one,) = plan(x[:1, :100])  # B == 1: the batch stride addresses nothing
+    assert one[2] == 1024
+    wide = torch.zeros(3, 40, 1536)[:, :, 256:1280]  # strided rows, uniform
+    (w1,) = plan(wide)
+    assert w1[2] == 1536
+    col = torch.zeros(4, 1, 256)  # S == 1: rows at the batch stride
+    (c1,) = plan(col)
+    assert c1[2] == 256
+
+
 def test_oracle_inputs_are_seeded_and_bf16_exact():
     a = ref.prologue_inputs(1, 1024, 2, seed=1001)
     b = ref.prologue_inputs(1, 1024, 2, seed=1001)

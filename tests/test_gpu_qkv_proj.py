@@ -5,10 +5,11 @@ restated by oracle.qkv_proj_norm_rope (float32 GEMM of the bf16 inputs, rounded
 to bf16, then the prologue). The kernel accumulates the GEMM in a different
 order, so a projection value near a bf16 rounding boundary can round the other
 way, and that one-ulp flip of the input carries through the normalisation as
-about one ulp of the output. Outputs are held to rel-L2 5e-3 and a max-abs bar
-of max(2e-2, 2^-7 max|expected|) (normalised q, k reach |4..8|, where one bf16
-ulp is 0.016..0.03); v, the projection output itself, to one bf16 ulp on
-nearly every element.
+about one ulp of the output. Normalised outputs are held to rel-L2 5e-3 and to
+max-abs 2e-2 on all but at most 0.1% of their elements; each of those few may
+be off by at most 2e-2 plus one bf16 ulp of its own value (normalised q, k
+reach |4..8|, where one ulp is 0.016..0.03). v, the projection output itself,
+is held to one bf16 ulp on nearly every element.
 """
 
 from __future__ import annotations
@@ -46,11 +47,31 @@ def _run(proj, hid, w, qw, kw, cos, sin, H, eps, dev="cuda:0"):
     return out
 
 
+MAX_FRAC_PAST_BAR = 1e-3  # elements allowed past max-abs 2e-2 (each within one more ulp)
+
+
+def _normed_parity(a, e, tag):
+    """rel-L2 5e-3; |a - e| <= 2e-2 on all but MAX_FRAC_PAST_BAR of the elements;
+    every element within 2e-2 + one bf16 ulp of its expected value."""
+    af, ef = a.detach().float().cpu(), e.detach().float().cpu()
+    assert torch.isfinite(af).all(), f"{tag}: non-finite values"
+    err = (af - ef).abs()
+    rl = ((af - ef).norm() / ef.norm().clamp_min(1e-30)).item()
+    past = (err > 2e-2).float().mean().item()
+    worst = (err - (2e-2 + ef.abs() * 2.0**-7)).max().item()
+    print(f"[parity] {tag}: max_abs={err.max().item():.3e} rel_l2={rl:.3e} past_2e-2={past:.2e}", flush=True)
+    assert rl <= 5e-3, f"{tag}: rel_l2 {rl:.3e} > 5e-3"
+    assert past <= MAX_FRAC_PAST_BAR, f"{tag}: {past:.2e} of elements past max-abs 2e-2"
+    assert worst <= 0, f"{tag}: an element is off by more than 2e-2 + one bf16 ulp"
+
+
 def _check(outs, exps, tag):
     for name, a, e in zip("qkv", outs, exps):
         assert a.dtype == BF and a.is_contiguous() and a.shape == e.shape
-        bar = max(2e-2, e.float().abs().max().item() * 2.0**-7)
-        parity(a, e.float(), max_abs=bar, name=f"{tag} {name}")
+        if name == "v":
+            parity(a, e.float(), name=f"{tag} {name}")
+        else:
+            _normed_parity(a, e, f"{tag} {name}")
     v, ev = outs[2].float().cpu(), exps[2].float()
     ulp = (v - ev).abs() <= ev.abs() * 2.0**-7 + 1e-30
     assert ulp.float().mean().item() > 0.999, f"{tag}: v beyond one bf16 ulp on {(~ulp).sum().item()} elements"
@@ -89,8 +110,7 @@ def test_qkv_proj_strided_rows_and_equals_unfused_path(pkg, proj):
         uq, uk, uv = pkg.qkv_norm_rope(qkv, qw.to(dev), kw.to(dev), cos.to(dev), sin.to(dev), H, 1e-6)
     torch.cuda.synchronize()
     for name, a, e in zip("qkv", outs, (uq, uk, uv)):
-        bar = max(2e-2, e.float().abs().max().item() * 2.0**-7)
-        parity(a, e.float().cpu(), max_abs=bar, name=f"fused vs unfused {name}")
+        _normed_parity(a, e, f"fused vs unfused {name}")
 
 
 def test_qkv_proj_rejects_bad_inputs(pkg, proj):
@@ -119,8 +139,8 @@ def test_qkv_proj_deterministic(pkg, proj):
 # proj_head_norm: q = head_norm(b.xq(hid), b.xq_norm, heads, eps) (src/model.py:324).
 # kv_proj_norm: k, v = b.xkv(ctx).view(B, S, 2, H, hd).unbind(2); k = F.rms_norm(k, ...)
 # (src/model.py:256-258). Oracle: oracle.proj_head_norm / oracle.kv_proj_norm; the
-# same bar as above (normalised outputs to rel-L2 5e-3 and max-abs max(2e-2, 2^-7 max),
-# the plain projection v to one bf16 ulp on nearly every element).
+# same bar as above (normalised outputs: _normed_parity; the plain projection v to
+# one bf16 ulp on nearly every element).
 
 
 def _lin_inputs(B, S, K, N, seed):
@@ -132,7 +152,7 @@ def _lin_inputs(B, S, K, N, seed):
 
 def _normed(a, e, tag):
     assert a.dtype == BF and a.is_contiguous() and a.shape == e.shape
-    parity(a, e.float(), max_abs=max(2e-2, e.float().abs().max().item() * 2.0**-7), name=tag)
+    _normed_parity(a, e, tag)
 
 
 @pytest.mark.parametrize(
@@ -207,6 +227,39 @@ def test_kv_proj_norm_equals_reference_expression(pkg, proj):
     torch.cuda.synchronize()
     _normed(k, uk.float().cpu(), "kv_proj_norm k vs torch")
     _normed(v, uv.float().cpu(), "kv_proj_norm v vs torch")
+
+
+@pytest.mark.parametrize("lens", [(58, 322), (200,), (512, 9)])
+def test_cross_projections_on_trimmed_context(pkg, proj, lens):
+    """trim_context's output (src/model.py:248-253) fed to kv_proj_norm, as
+    encode_context does (model.py:256-258): ctx[:, :keep] is a view whose batch
+    stride is S * K, not keep * K. Also proj_head_norm on a batch-strided view."""
+    B, S, H, K = len(lens), 512, 16, 1024
+    ctx, w, kw = _lin_inputs(B, S, K, 2 * H * 128, seed=1650 + sum(lens))
+    for b, n in enumerate(lens):
+        ctx[b, n:] = 0
+    dev = "cuda:0"
+    trimmed, seqused, _ = pkg.trim_context(ctx.to(dev, BF))
+    keep = trimmed.shape[1]
+    assert keep == min(S, (max(lens) + 7) // 8 * 8)
+    if B > 1 and keep < S:
+        assert trimmed.stride(0) == S * K and not trimmed.is_contiguous()
+    kw16 = kw.to(BF)
+    with torch.no_grad():
+        k, v = proj.kv_proj_norm(trimmed, w.to(dev), kw16.to(dev), H, 1e-6)
+    torch.cuda.synchronize()
+    assert torch.equal(seqused.cpu(), torch.tensor(lens, dtype=torch.int32))
+    ek, ev = ref.kv_proj_norm(ctx[:, :keep], w, kw16, H, 1e-6)
+    _normed(k, ek, f"kv_proj_norm on trimmed ctx lens={lens}")
+    vc = v.float().cpu()
+    ulp = (vc - ev).abs() <= ev.abs() * 2.0**-7 + 1e-30
+    assert ulp.float().mean().item() > 0.999, f"v beyond one bf16 ulp on {(~ulp).sum().item()} elements"
+    # The query side on a batch-strided view (every other item of a larger batch).
+    xq, wq, nq = _lin_inputs(2 * B, 300, 2048, H * 128, seed=1660 + sum(lens))
+    with torch.no_grad():
+        y = proj.proj_head_norm(xq.to(dev, BF)[::2], wq.to(dev), nq.to(dev), H, 1e-6)
+    torch.cuda.synchronize()
+    _normed(y, ref.proj_head_norm(xq[::2], wq, nq, H, 1e-6), f"proj_head_norm batch-strided lens={lens}")
 
 
 def test_cross_projections_reject_bad_inputs(pkg, proj):

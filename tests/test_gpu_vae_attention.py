@@ -97,6 +97,29 @@ def test_d384_lse_mask_and_padding_correction(pkg):
     parity(corr, ref.ctx_scale(eo, el, ln_pad), name="d384 padding correction")
 
 
+def test_d384_no_keys_gives_zero_output(pkg):
+    """Sk == 0 at head_dim 384 behaves as at head_dim 128: O = 0, LSE = -inf; and
+    a batch item whose key length is 0 gets the same while the other attends."""
+    A = importlib.import_module("anima_flat_amd.attention")
+    q = torch.randn(2, 300, 1, D, device=DEV).to(BF)
+    kv = torch.randn(2, 1, 1, D, device=DEV).to(BF)[:, :0]
+    out, lse = A._launch_fwd(q, kv, kv, want_lse=True, head_dims=(D,))
+    torch.cuda.synchronize()
+    assert out.shape == q.shape and torch.equal(out.cpu(), torch.zeros(q.shape, dtype=BF))
+    assert torch.isneginf(lse.cpu()).all()
+    g = torch.Generator().manual_seed(399)
+    qc, kc, vc = (ref.bf16_normal((2, S, 1, D), g) for S in (300, 200, 200))
+    lens = torch.tensor([0, 150], dtype=torch.int32)
+    out, lse = A._launch_fwd(qc.to(DEV, BF), kc.to(DEV, BF), vc.to(DEV, BF), want_lse=True,
+                             seqused_k=lens.to(DEV), head_dims=(D,))
+    torch.cuda.synchronize()
+    assert torch.equal(out[0].cpu(), torch.zeros(300, 1, D, dtype=BF))
+    assert torch.isneginf(lse[0].cpu()).all()
+    eo, el = ref.attention_lse(qc[1:], kc[1:, :150], vc[1:, :150])
+    parity(out[1:], eo, name="d384 item with 150 keys")
+    torch.testing.assert_close(lse[1:].cpu(), el, atol=2e-3, rtol=0)
+
+
 def test_d384_split_and_unsplit_agree(pkg, vae):
     """Batch item 0 alone (32 work items: keys split 8 ways, combine pass) and
     inside a batch of 8 (256 work items: no split) give the same result."""
