@@ -28,6 +28,8 @@
 // The transposed reads list the keys / queries of each 16-column chunk in the
 // accumulator row order, so the bf16-rounded accumulators are the B operands
 // as they are.
+#include <algorithm>
+
 #include "tile_io.h"
 
 namespace aa {
@@ -52,6 +54,12 @@ struct Params {
   bf16* dv;
   int64_t s_do[3], s_q[3], s_k[3], s_v[3], s_o[3], s_dq[3], s_dk[3], s_dv[3];
   float* stats;  // [B][H][ntq][kStat]
+  // Query split of dkdv_kernel (see dkdv_split): with nsplit > 1, workgroup
+  // (split, b, h, key block) covers query tiles split * ceil(ntq / nsplit) ..
+  // and writes its fp32 dV^T / dK^T accumulators to part (layout at
+  // dkdv_combine_kernel), which the combine pass sums in a fixed order.
+  float* part;
+  int nsplit;
   int H, Sq, Sk, ntq, ntk;
   float c;      // scale * log2(e)
   float scale;  // softmax scale
@@ -94,8 +102,11 @@ void dkdv_kernel(Params p, int nkblk, int total_blocks) {
   __shared__ __attribute__((aligned(1024))) bf16x8 pslot[4][4][64];  // [pair][c4][lane]
 
   const int logical = xcd_remap(blockIdx.x, total_blocks);
-  const int kblk = logical % nkblk;
-  const int bh = logical / nkblk;
+  const int per_split = total_blocks / p.nsplit;
+  const int split = logical / per_split;
+  const int rest = logical - split * per_split;
+  const int kblk = rest % nkblk;
+  const int bh = rest / nkblk;
   const int b = bh / p.H, h = bh - (bh / p.H) * p.H;
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -117,8 +128,11 @@ void dkdv_kernel(Params p, int nkblk, int total_blocks) {
 
   const bf16* qbase = p.q + b * p.s_q[0] + h * p.s_q[2];
   const bf16* dobase = p.dout + b * p.s_do[0] + h * p.s_do[2];
-  const float* statb = p.stats + (int64_t)bh * p.ntq * kStat;
-  const int ntiles = p.ntq;
+  // Query tiles tq0 .. tq0 + ntiles - 1 (all of them without a split).
+  const int tper = (p.ntq + p.nsplit - 1) / p.nsplit;
+  const int tq0 = min(split * tper, p.ntq);
+  const int ntiles = min(tper, p.ntq - tq0);
+  const float* statb = p.stats + ((int64_t)bh * p.ntq + tq0) * kStat;
 
   // DMA by the B waves, g = wave - 4: blocks 4 g .. 4 g + 3 of the Q and dO
   // dual line tiles (8 rows x 128 bytes per instruction); wave 4 also copies
@@ -129,7 +143,7 @@ void dkdv_kernel(Params p, int nkblk, int total_blocks) {
   qdma.setup(g, lane, p.s_q[1]);
   dodma.setup(g, lane, p.s_do[1]);
   auto issue_tile = [&](int t) {
-    const int st = t % kDkStages, q0 = t * kT, nr = min(kT, p.Sq - q0);
+    const int st = t % kDkStages, q0 = (tq0 + t) * kT, nr = min(kT, p.Sq - q0);
     qdma.issue(qbase + (int64_t)q0 * p.s_q[1], p.s_q[1], nr, rows[st][0], lane);
     dodma.issue(dobase + (int64_t)q0 * p.s_do[1], p.s_do[1], nr, rows[st][1], lane);
     if (wave == 4) dma16(statb + (int64_t)t * kStat + 4 * lane, stat[st]);
@@ -275,10 +289,56 @@ void dkdv_kernel(Params p, int nkblk, int total_blocks) {
   // dV (A) / dK (B) rows out through LDS staging: the stages of tiles
   // ntiles-4 and ntiles-3 are free (B may still be reading tile ntiles-1 in
   // its final M block; no DMA is in flight).
+  if (p.nsplit > 1) {
+    // Partial accumulators, 16 coalesced 1 KB stores per wave: float4 j of
+    // lane l at ((logical * 8 + wave) * 16 + j) * 64 + l.
+    f32x4* dst = reinterpret_cast<f32x4*>(p.part) + ((int64_t)logical * kDkWaves + wave) * 16 * 64 + lane;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const f32x4 v4 = {acc[j >> 2][4 * (j & 3)], acc[j >> 2][4 * (j & 3) + 1], acc[j >> 2][4 * (j & 3) + 2],
+                        acc[j >> 2][4 * (j & 3) + 3]};
+      __builtin_nontemporal_store(v4, dst + j * 64);
+    }
+    return;
+  }
   bf16* ostage = &rows[(ntiles + (wave >> 2)) % kDkStages][0][0] + (wave & 3) * 4096;
   stage_acc_rows(acc, role_a ? 1.0f : p.scale, lane, ostage);
   if (role_a) stage_rows_out(p.dv + b * p.s_dv[0] + h * p.s_dv[2], p.s_dv[1], key0, p.Sk, lane, ostage);
   else stage_rows_out(p.dk + b * p.s_dk[0] + h * p.s_dk[2], p.s_dk[1], key0, p.Sk, lane, ostage);
+}
+
+// Sums the query-split partials of dkdv_kernel in split order and writes dV
+// and dK (times the softmax scale) as bf16. One thread per float4 of a
+// workgroup's partial (wave w, lane l, j): accumulator block dt = j / 4,
+// registers 4 (j % 4) .. + 3, i.e. key 32 (w % 4) + l % 32 of the key block
+// and head-dim 32 dt + 8 (j % 4) + 4 (l / 32) .. + 3; waves 0-3 hold dV^T,
+// 4-7 dK^T.
+__global__ __launch_bounds__(256) void dkdv_combine_kernel(Params p, int nkblk, int per_split) {
+  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;  // (rest, wave, j, lane)
+  const int lane = (int)(gid & 63);
+  const int j = (int)((gid >> 6) & 15);
+  const int wave = (int)((gid >> 10) & 7);
+  const int rest = (int)(gid >> 13);
+  if (rest >= per_split) return;
+  const int kblk = rest % nkblk, bh = rest / nkblk;
+  const int b = bh / p.H, h = bh - b * p.H;
+  const int key = kblk * kKeysPerWg + (wave & 3) * 32 + (lane & 31);
+  if (key >= p.Sk) return;
+  const f32x4* src = reinterpret_cast<const f32x4*>(p.part) + (((int64_t)rest * kDkWaves + wave) * 16 + j) * 64 + lane;
+  const int64_t split_stride = (int64_t)per_split * kDkWaves * 16 * 64;
+  f32x4 sum = src[0];
+  for (int s = 1; s < p.nsplit; ++s) {
+    const f32x4 v4 = src[s * split_stride];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sum[i] += v4[i];
+  }
+  const bool is_dv = wave < 4;
+  const float sc = is_dv ? 1.0f : p.scale;
+  const int d0 = 32 * (j >> 2) + 8 * (j & 3) + 4 * (lane >> 5);
+  bf16* out = is_dv ? p.dv + b * p.s_dv[0] + (int64_t)key * p.s_dv[1] + h * p.s_dv[2]
+                    : p.dk + b * p.s_dk[0] + (int64_t)key * p.s_dk[1] + h * p.s_dk[2];
+  const u32x2 w = {pack_bf16(sum[0] * sc, sum[1] * sc), pack_bf16(sum[2] * sc, sum[3] * sc)};
+  *reinterpret_cast<u32x2*>(out + d0) = w;
 }
 
 // ------------------------------------------------------------------ dQ --
@@ -518,16 +578,34 @@ static bool stride_ok(const int64_t* s) {
          s[1] < (1ll << 40) && s[2] < (1ll << 40);
 }
 
+// Query splits of dkdv_kernel: when its workgroups (one per 128 keys of each
+// (batch, head)) fill at most half of the CUs, as for the 512-key text
+// context at B = 2 and 16 heads (128 workgroups), each key block's query
+// tiles are split over up to 4 workgroups, each covering at least 4 tiles.
+static int dkdv_split(int64_t B, int64_t Sq, int64_t Sk, int64_t H, int ncu) {
+  const int64_t blocks = B * H * ((Sk + kKeysPerWg - 1) / kKeysPerWg);
+  const int64_t ntq = (Sq + kT - 1) / kT;
+  if (ncu <= 0 || blocks <= 0 || 2 * blocks > ncu) return 1;
+  int64_t ns = std::min<int64_t>(4, ncu / blocks);
+  ns = std::min<int64_t>(ns, ntq / 4);
+  return (int)std::max<int64_t>(ns, 1);
+}
+
 struct WsLayout {
-  size_t stats, total;
+  size_t stats, part, total;
+  int nsplit;
 };
 
 static WsLayout ws_layout(int64_t B, int64_t Sq, int64_t Sk, int64_t H) {
-  (void)Sk;
   const int64_t ntq = (Sq + kT - 1) / kT;
   WsLayout w;
+  w.nsplit = dkdv_split(B, Sq, Sk, H, device_cu_count());
   w.stats = 0;
-  w.total = w.stats + (size_t)(B * H * ntq) * kStat * sizeof(float);
+  w.part = w.stats + (size_t)(B * H * ntq) * kStat * sizeof(float);
+  const int64_t blocks = B * H * ((Sk + kKeysPerWg - 1) / kKeysPerWg);
+  const size_t part_bytes =
+      w.nsplit > 1 ? (size_t)w.nsplit * blocks * kDkWaves * 64 * 64 * sizeof(float) : 0;
+  w.total = w.part + part_bytes;
   return w;
 }
 
@@ -598,6 +676,8 @@ extern "C" int aa_attn_bwd(const aa_attn_bwd_args* a, void* workspace, size_t wo
   }
   char* ws = (char*)workspace;
   p.stats = (float*)(ws + wl.stats);
+  p.part = (float*)(ws + wl.part);
+  p.nsplit = wl.nsplit;
   p.H = (int)a->H;
   p.Sq = (int)a->Sq;
   p.Sk = (int)a->Sk;
@@ -618,9 +698,15 @@ extern "C" int aa_attn_bwd(const aa_attn_bwd_args* a, void* workspace, size_t wo
   }
   if (a->Sk > 0) {
     const int nkblk = (int)((a->Sk + bwd::kKeysPerWg - 1) / bwd::kKeysPerWg);
-    const int total = (int)(BH * nkblk);
+    const int per_split = (int)(BH * nkblk);
+    const int total = per_split * p.nsplit;
     bwd::dkdv_kernel<<<dim3((unsigned)total), bwd::kDkWaves * 64, 0, st>>>(p, nkblk, total);
     if (int rc = check_launch("attn_bwd dkdv")) return rc;
+    if (p.nsplit > 1) {
+      const int64_t threads = (int64_t)per_split * bwd::kDkWaves * 16 * 64;
+      bwd::dkdv_combine_kernel<<<dim3((unsigned)(threads / 256)), 256, 0, st>>>(p, nkblk, per_split);
+      if (int rc = check_launch("attn_bwd dkdv combine")) return rc;
+    }
   }
   return AA_OK;
 }

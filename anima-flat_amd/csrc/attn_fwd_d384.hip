@@ -142,7 +142,8 @@ struct Wave {
   bf16x8 pb[2];     // P^T of the current tile, keys 0-15 and 16-31
   float m_raw;      // running row max in raw score units
   float mt;         // row max of the next tile (raw)
-  float l[2];       // this lane's share of the row sum, two chains
+  f32x4 lsum;       // row sum of query li (all four elements), by MFMA
+  bf16x8 sel;       // 0/1 selector: the A operand of the row-sum MFMA
   float c, thr_raw;
   int li, hh, k_rd, v_tr0, v_tr1;
 
@@ -161,7 +162,17 @@ struct Wave {
       asm volatile("" : "+a"(o[db]));
     }
     m_raw = -INFINITY;
-    l[0] = l[1] = 0.f;
+    lsum = f32x4{};
+    // Row sums by v_mfma_f32_16x16x32_bf16 with the P^T operand as B: in that
+    // shape lane l's 8 values are B[k = 8 (l / 16) + i][n = l % 16], i.e.
+    // query n (+16 for odd l / 16) over one half of the chunk's keys. With
+    // A[m][k] = 1 where bit 2 of m equals bit 3 of k, D[m][n] sums query n
+    // for m % 8 < 4 and query n + 16 otherwise, which puts the row sum of
+    // query li in all four D values of the lane. (v_dot2c_f32_bf16 over the
+    // bf16 pairs would stall the matrix pipe for about half an MFMA each.)
+    const bf16 one = (bf16)(((lane & 15) >> 2 & 1) == ((lane >> 4) & 1) ? 1.0f : 0.0f);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) sel[i] = one;
   }
 
   // Operand reads address LDS as one pinned 32-bit byte base per tile (two
@@ -243,7 +254,6 @@ struct Wave {
   template <bool QK>
   __device__ __forceinline__ void phase1(const bf16* kst, const DmaJob& job) {
     const float mc = m_raw * c;
-    const bf16x2 ones = {(bf16)1.0f, (bf16)1.0f};
     bf16x8 q[kPf];
     float pf = 0.f;
     const uint32_t kb = QK ? k_base(kst) : 0u;
@@ -263,13 +273,15 @@ struct Wave {
         } else {
           pb[i >> 3][(i & 7) - 1] = (bf16)pf;
           pb[i >> 3][i & 7] = (bf16)e;
-          const bf16x2 pair = {pb[i >> 3][(i & 7) - 1], pb[i >> 3][i & 7]};
-          l[(i >> 1) & 1] = __builtin_amdgcn_fdot2_f32_bf16(pair, ones, l[(i >> 1) & 1], false);
           // Anchored in this slot: left alone, the compiler sinks the whole
           // P computation into phase 2, next to its MFMA users, where it
           // stalls them instead of overlapping phase 1's.
-          asm volatile("" : "+v"(pb[i >> 3]), "+v"(l[(i >> 1) & 1]));
+          asm volatile("" : "+v"(pb[i >> 3]));
         }
+      }
+      // The row sums of a finished P^T operand (16 keys), on the matrix pipe.
+      if constexpr (i == 8 || i == 16) {
+        lsum = __builtin_amdgcn_mfma_f32_16x16x32_bf16(sel, pb[(i >> 3) - 1], lsum, 0, 0, 0);
       }
       __builtin_amdgcn_sched_barrier(0);
     });
@@ -325,13 +337,13 @@ struct Wave {
         for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
         asm volatile("" : "+a"(o[db]));
       }
-      l[0] *= alpha;
-      l[1] *= alpha;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) lsum[r] *= alpha;
       m_raw = mn;
     }
   }
 
-  __device__ __forceinline__ float row_sum() const { return pair_sum(l[0] + l[1]); }
+  __device__ __forceinline__ float row_sum() const { return lsum[0]; }
 };
 
 // Block -> (item, split): logical index L = xcd_remap(block) runs split-major,

@@ -135,7 +135,7 @@ def copy_calibration(dev) -> None:
 
 PROFILE_CASES = ("self_cfg2", "self_cfg1", "prologue_cfg2", "head_norm_cfg3", "cross_cfg3",
                  "cross_b2_512", "rowquant_cfg3", "prologue_bwd_cfg5", "vae_d384", "qkv_proj_cfg2", "qkv_proj_b2",
-                 "xq_proj_cfg3", "xkv_proj_cfg3", "fwd_bwd_cfg5")
+                 "xq_proj_cfg3", "xkv_proj_cfg3", "fwd_bwd_cfg5", "cross_fwd_bwd_b2")
 
 
 def profile_case(name: str, steps: int, pkg, fp8, dev) -> dict:
@@ -153,6 +153,18 @@ def profile_case(name: str, steps: int, pkg, fp8, dev) -> dict:
         for _ in range(steps):
             out = pkg.attention(qg, kg, vg)
             torch.autograd.grad(out, (qg, kg, vg), dout)
+        torch.cuda.synchronize()
+        return {"profile_case": name, "steps": steps}
+    if name == "cross_fwd_bwd_b2":
+        qc = torch.randn(2, S, H, d, device=dev, dtype=BF).requires_grad_(True)
+        kvc = torch.randn(2, 512, 2, H, d, device=dev, dtype=BF)
+        kvc[0, 58:] = 0
+        kvc[1, 322:] = 0
+        kvc.requires_grad_(True)
+        doc = torch.randn(2, S, H * d, device=dev, dtype=BF)
+        for _ in range(steps):
+            out = pkg.attention(qc, kvc[:, :, 0], kvc[:, :, 1])
+            torch.autograd.grad(out, (qc, kvc), doc)
         torch.cuda.synchronize()
         return {"profile_case": name, "steps": steps}
     if name in ("self_cfg2", "self_cfg1", "prologue_cfg2", "prologue_bwd_cfg5"):
@@ -543,6 +555,29 @@ def main() -> int:
         }
 
         if args.extras == "all":
+            # LoRA training's cross-attention: forward + backward at B=2 (CFG is off in
+            # training, but the batch holds 2 items here), 4096 queries over the 512-key
+            # zero-padded text context, which training does not trim (src/model.py:326).
+            qc = torch.randn(2, S, H, d, device=dev, dtype=BF).requires_grad_(True)
+            kvc = torch.randn(2, 512, 2, H, d, device=dev, dtype=BF)
+            kvc[0, 58:] = 0
+            kvc[1, 322:] = 0
+            kvc.requires_grad_(True)
+            doc = torch.randn(2, S, H * d, device=dev, dtype=BF)
+
+            def cross_fwd_bwd():
+                out = pkg.attention(qc, kvc[:, :, 0], kvc[:, :, 1])
+                torch.autograd.grad(out, (qc, kvc), doc)
+
+            prewarm(cross_fwd_bwd, 0.2)
+            _, us_cb = time_launches(cross_fwd_bwd, max(5, steps // 2), 2)
+            cb_flops = 3.5 * attn_flops(2, H, S, 512)
+            extras["cross_fwd_bwd_b2_sk512"] = {
+                "us": round(us_cb * 1e3, 2),
+                "TFLOP/s": round(cb_flops / (us_cb * 1e-3) / 1e12, 1),
+                "pct_of_peak": round(100 * cb_flops / (us_cb * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 2),
+            }
+
             # One CFG denoiser step at 1024x1024: 28 layers x (prologue + self-attn B=2 S=4096
             # + head_norm + cross-attn over 512 untrimmed keys).
             p2 = prologue_qkv(pkg, 2, S, H, 1010, dev)

@@ -334,3 +334,33 @@ def test_long_sequence_backward_sampled_rows(pkg):
     parity(qd.grad[:, qrows], dq, name="long dq")
     parity(kd.grad[:, krows], dk, name="long dk")
     parity(vd.grad[:, krows], dv, name="long dv")
+
+
+def test_cross_attention_backward_training_shape(pkg):
+    """LoRA training's cross-attention backward: fa_bwd at B=2, Sq=4096, Sk=512 over
+    the untrimmed, zero-padded text context (src/model.py:326 -> src/attention.py
+    :143-146, :118-120; the context is not trimmed under grad). Projecting a zero
+    context row and RMS-normalising its key gives zero K and V rows, which still
+    take part in the softmax (score 0). dQ on 64 sampled query rows of each item,
+    dK/dV on 64 sampled key rows that include padded ones, against the chunked
+    closed-form oracle."""
+    B, Sq, Sk, H = 2, 4096, 512, 16
+    q, k, v = _qkv(B, Sq, Sk, H, seed=4099)
+    for b, n in enumerate((58, 322)):
+        k[b, n:] = 0
+        v[b, n:] = 0
+    g = torch.Generator().manual_seed(4100)
+    dout = ref.bf16_normal((B, Sq, H, 128), g)
+    qd, kd, vd = (t.requires_grad_(True) for t in _gpu(q, k, v))
+    out = pkg.attention(qd, kd, vd)
+    out.backward(dout.to("cuda", BF).reshape(out.shape))
+    torch.cuda.synchronize()
+    qrows = torch.randperm(Sq, generator=g)[:64].sort().values
+    krows = torch.cat([torch.tensor([0, 57, 58, 321, 322, Sk - 1]),
+                       torch.randperm(Sk, generator=g)[:58]]).unique().sort().values
+    dq, dk, dv = ref.attention_backward_rows(q, k, v, dout, qrows, krows)
+    parity(qd.grad[:, qrows], dq, name="cross bwd dq")
+    parity(kd.grad[:, krows], dk, name="cross bwd dk")
+    parity(vd.grad[:, krows], dv, name="cross bwd dv")
+    eo = ref.attention_lse(q[:, qrows], k, v)[0]
+    parity(out.reshape(B, Sq, H, 128)[:, qrows], eo, name="cross fwd (sampled rows)")
