@@ -24,7 +24,7 @@ LIB_NAME = "libanima_attn.so"
 LIB_PATH = HERE / LIB_NAME
 SOURCES = (
     "abi.hip", "prologue.hip", "ctx_scale.hip", "context.hip", "rowquant.hip", "attn_fwd.hip",
-    "attn_fwd_d384.hip", "attn_bwd.hip", "qkv_proj.hip",
+    "attn_fwd_pp.hip", "attn_fwd_d384.hip", "attn_bwd.hip", "qkv_proj.hip",
 )
 ARCH = "gfx950"
 

@@ -69,63 +69,19 @@
 #include <string>
 #include <type_traits>
 
+#include "attn_fwd.h"
 #include "attn_fwd_d384.h"
 #include "tile_io.h"
 
 namespace aa {
 
-constexpr int kD = 128;
-constexpr int kBN = 64;                      // keys per tile
-constexpr float kRescaleThreshold = 8.0f;    // log2 units
 constexpr int kWaves = 4;                    // one per SIMD
 constexpr int kQPerWave = 64;                // two blocks of 32 queries
-constexpr int kQPerWg = kWaves * kQPerWave;  // 256 queries per work item
+static_assert(kWaves * kQPerWave == kQPerWg, "work item size");
 constexpr int kStages = 4;                   // K/V ring depth (4 x 32 KB)
 constexpr int kLead = kStages - 1;           // tile t + kLead is fetched during tile t
 constexpr uint32_t kStageBytes = 2u * kTileElems * sizeof(bf16);  // K tile, then V tile
 constexpr uint32_t kVOff = kTileElems * sizeof(bf16);             // V tile in a stage
-
-struct FwdParams {
-  const bf16* q;
-  const bf16* k;
-  const bf16* v;
-  bf16* o;
-  float* lse;
-  const int32_t* seqused;
-  const float* ln_pad;
-  int64_t qs0, qs1, qs2;
-  int64_t ks0, ks1, ks2;
-  int64_t vs0, vs1, vs2;
-  int64_t os0, os1, os2;
-  int H, Sq, Sk, nqblk, total_blocks;
-  float c;  // softmax_scale * log2(e)
-  // Key split of the last work items (see split_plan): blocks past full_blocks
-  // each take one of nsplit key ranges of work item full_blocks + j / nsplit
-  // and write normalised partials (part_o [j][split][256][128] bf16,
-  // part_lse [j][split][256] fp32) that attn_fwd_combine_kernel merges.
-  int full_blocks, split_items, nsplit;
-  // Workgroups resident at once (one per CU): the unsplit blocks are mapped
-  // to work items round by round (see attn_fwd_kernel).
-  int round_blocks;
-  bf16* part_o;
-  float* part_lse;
-};
-
-// (batch, head, query block) of one work item; klen keys attended.
-struct Item {
-  int b, h, qblk, klen, ntiles;
-};
-
-__device__ __forceinline__ Item decode_item(const FwdParams& p, int it) {
-  Item r;
-  r.qblk = it % p.nqblk;
-  const int bh = it / p.nqblk;
-  r.b = bh / p.H;
-  r.h = bh - r.b * p.H;
-  r.klen = p.seqused ? min((int)p.seqused[r.b], p.Sk) : p.Sk;
-  r.ntiles = r.klen > 0 ? (r.klen + kBN - 1) / kBN : 0;
-  return r;
-}
 
 // K/V tile DMA of one wave into the K and V line tiles of a ring stage
 // (tile_io.h). A DMA instruction fills one 1 KB block = 8 rows x 64 d from 8
@@ -565,23 +521,8 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(1, 
 void attn_fwd_kernel(FwdParams p) {
   __shared__ __attribute__((aligned(1024))) bf16 kv_lds[kStages * 2 * kTileElems];
 
-  // Block -> work item. Blocks start in index order, so block r * R + j
-  // (R = round_blocks) runs in round r: it takes an item of that round's
-  // range [r R, r R + R), XCD-aware within the round (the query blocks of one
-  // head share an XCD and its L2). Mapping over the whole grid instead would
-  // mix items of every batch into each round, and with per-batch key lengths
-  // (seqused) every round would then last as long as the longest item.
-  int item_idx, split = -1;
-  if ((int)blockIdx.x < p.full_blocks) {
-    const int r = (int)blockIdx.x / p.round_blocks;
-    const int j = (int)blockIdx.x - r * p.round_blocks;
-    const int in_round = min(p.round_blocks, p.full_blocks - r * p.round_blocks);
-    item_idx = r * p.round_blocks + xcd_remap(j, in_round);
-  } else {
-    const int j = blockIdx.x - p.full_blocks;
-    item_idx = p.full_blocks + j / p.nsplit;
-    split = j - (j / p.nsplit) * p.nsplit;
-  }
+  int item_idx, split;
+  block_item(p, item_idx, split);
   const Item it = decode_item(p, item_idx);
   // Key tiles [t0, t0 + ntiles) of the item.
   int t0 = 0, ntiles = it.ntiles;
@@ -904,6 +845,25 @@ static int fwd_scratch(void** out) {
   return AA_OK;
 }
 
+// Which head_dim-128 kernel runs: the two-group kernel of attn_fwd_pp.hip (0)
+// up to kPingPongMaxSk keys, where a work item's fixed costs weigh most, and
+// this file's one-wave-per-SIMD kernel (1) beyond. Measured on MI355X at
+// B = 1-2, 4096 queries: the two-group kernel is 5-8% faster at 512 and 1024
+// keys, the two tie at 2048, the one-wave kernel is ~3% faster at 4096.
+// AA_FWD_KERNEL=pp|1w forces one (tests run both on every shape); -1 for
+// another value.
+constexpr int64_t kPingPongMaxSk = 2048;
+static int fwd_kernel_choice(int64_t Sk) {
+  const char* e = std::getenv("AA_FWD_KERNEL");
+  if (e && *e) {
+    const std::string v = e;
+    if (v == "pp") return 0;
+    if (v == "1w") return 1;
+    return -1;
+  }
+  return Sk <= kPingPongMaxSk ? 0 : 1;
+}
+
 extern "C" int aa_attn_fwd(const aa_attn_fwd_args* a, void* stream);
 
 extern "C" int aa_attn_fwd_noalloc(const aa_attn_fwd_args* a, void* stream) {
@@ -937,7 +897,10 @@ extern "C" int aa_attn_fwd(const aa_attn_fwd_args* a, void* stream) {
   if (a->B == 0 || a->Sq == 0) return AA_OK;
   hipStream_t st = (hipStream_t)stream;
   const int blocks = p.full_blocks + p.split_items * p.nsplit;
-  attn_fwd_kernel<<<dim3((unsigned)blocks), kWaves * 64, 0, st>>>(p);
+  const int which = fwd_kernel_choice(p.Sk);
+  if (which < 0) return fail(AA_EINVAL, "AA_FWD_KERNEL must be pp or 1w");
+  if (which == 0) launch_attn_fwd_pp(p, (unsigned)blocks, st);
+  else attn_fwd_kernel<<<dim3((unsigned)blocks), kWaves * 64, 0, st>>>(p);
   if (int rc = check_launch("attn_fwd")) return rc;
   if (p.split_items > 0) {
     const int groups = (p.split_items * kQPerWg + kCombineQ - 1) / kCombineQ;

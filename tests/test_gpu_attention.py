@@ -364,3 +364,41 @@ def test_cross_attention_backward_training_shape(pkg):
     parity(vd.grad[:, krows], dv, name="cross bwd dv")
     eo = ref.attention_lse(q[:, qrows], k, v)[0]
     parity(out.reshape(B, Sq, H, 128)[:, qrows], eo, name="cross fwd (sampled rows)")
+
+
+@pytest.mark.parametrize("kernel", ["pp", "1w"])
+@pytest.mark.parametrize(
+    "B,Sq,Sk,H,lens",
+    [
+        (1, 1024, 1024, 16, None),  # config 1: 64 work items, split over key ranges
+        (2, 4096, 512, 4, [58, 322]),  # config 3's masked cross-attention
+        (1, 300, 777, 3, None),  # ragged: partial query and key tiles
+        (2, 700, 2500, 2, [2500, 1]),  # one key; a key length past 2048
+        (1, 4096, 4096, 2, None),  # long: 64 key tiles
+    ],
+)
+def test_both_forward_kernels(pkg, monkeypatch, kernel, B, Sq, Sk, H, lens):
+    """aa_attn_fwd runs the two-group kernel up to 2048 keys and the one-wave-per-SIMD
+    kernel beyond (AA_FWD_KERNEL forces one); each is held to the oracle on every
+    shape, with and without key lengths, and its LSE."""
+    q, k, v = _qkv(B, Sq, Sk, H, seed=9000 + Sq + Sk + H)
+    seq = torch.tensor(lens, dtype=torch.int32) if lens is not None else None
+    monkeypatch.setenv("AA_FWD_KERNEL", kernel)
+    qd, kd, vd = _gpu(q, k, v)
+    if seq is None:
+        out, lse = torch.ops.anima_flat.fa_fwd(qd, kd, vd)
+    else:
+        out, lse = torch.ops.anima_flat.fa_fwd_k(qd, kd, vd, seq.to("cuda"))
+    torch.cuda.synchronize()
+    monkeypatch.delenv("AA_FWD_KERNEL")
+    eo, el = ref.attention_lse(q, k, v, seq)
+    tag = f"{kernel} B{B} Sq{Sq} Sk{Sk} H{H} lens={lens}"
+    parity(out, eo, name=tag)
+    parity(lse, el, **LSE_TOL, name=f"lse {tag}")
+
+
+def test_forward_kernel_env_rejects_unknown_value(pkg, monkeypatch):
+    q, k, v = _gpu(*_qkv(1, 64, 64, 1, seed=9100))
+    monkeypatch.setenv("AA_FWD_KERNEL", "zz")
+    with pytest.raises(ValueError, match="AA_FWD_KERNEL"):
+        torch.ops.anima_flat.fa_fwd(q, k, v)
