@@ -24,6 +24,24 @@ __device__ __forceinline__ void load_section(const bf16* src, int j, Section& s)
   unpack8(ld16(src + kHalf + 8 * j), s.b);
 }
 
+// A section's two 16-byte chunks as loaded, before unpacking.
+struct RawSection {
+  u32x4 a;
+  u32x4 b;
+};
+
+__device__ __forceinline__ void load_raw(const bf16* src, int j, RawSection& r) {
+  r.a = ld16(src + 8 * j);
+  r.b = ld16(src + kHalf + 8 * j);
+}
+
+__device__ __forceinline__ Section unpack_section(const RawSection& r) {
+  Section s;
+  unpack8(r.a, s.a);
+  unpack8(r.b, s.b);
+  return s;
+}
+
 __device__ __forceinline__ void load_w(const float* w, int j, float* wa, float* wb) {
   f32x4 w0 = ldf4(w + 8 * j), w1 = ldf4(w + 8 * j + 4);
   f32x4 w2 = ldf4(w + kHalf + 8 * j), w3 = ldf4(w + kHalf + 8 * j + 4);
@@ -50,13 +68,9 @@ __device__ __forceinline__ void load_rot(const float* cos, const float* sin, int
   }
 }
 
-// rstd over the section's 128 values, y = bf16(x * rstd * w), then with
-// ROTATE out_a = y_a cos - y_b sin, out_b = y_b cos + y_a sin (the order of
-// src/kernels/rope.py:39-58).
-template <bool ROTATE>
-__device__ __forceinline__ void norm_rotate(const Section& x, const float* w, const float* cos,
-                                            const float* sin, int64_t pos, int j, float eps,
-                                            float* oa, float* ob) {
+// rstd over the section's 128 values, y = bf16(x * rstd * w).
+__device__ __forceinline__ void norm_scale(const Section& x, const float* w, int j, float eps,
+                                           float* oa, float* ob) {
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) ss += x.a[i] * x.a[i] + x.b[i] * x.b[i];
@@ -69,15 +83,29 @@ __device__ __forceinline__ void norm_rotate(const Section& x, const float* w, co
     oa[i] = round_bf16(x.a[i] * rstd * wa[i]);
     ob[i] = round_bf16(x.b[i] * rstd * wb[i]);
   }
+}
+
+// out_a = y_a cos - y_b sin, out_b = y_b cos + y_a sin (the order of
+// src/kernels/rope.py:39-58), in place, with this lane's 8 cos / sin values.
+__device__ __forceinline__ void rotate_half(float* a, float* b, const float* c, const float* s) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float ya = a[i], yb = b[i];
+    a[i] = ya * c[i] - yb * s[i];
+    b[i] = yb * c[i] + ya * s[i];
+  }
+}
+
+// norm_scale, then with ROTATE rotate_half by the RoPE row of position pos.
+template <bool ROTATE>
+__device__ __forceinline__ void norm_rotate(const Section& x, const float* w, const float* cos,
+                                            const float* sin, int64_t pos, int j, float eps,
+                                            float* oa, float* ob) {
+  norm_scale(x, w, j, eps, oa, ob);
   if constexpr (ROTATE) {
     float c[8], s[8];
     load_rot(cos, sin, pos, j, c, s);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float ya = oa[i], yb = ob[i];
-      oa[i] = ya * c[i] - yb * s[i];
-      ob[i] = yb * c[i] + ya * s[i];
-    }
+    rotate_half(oa, ob, c, s);
   }
 }
 

@@ -6,6 +6,7 @@
 // [8j, 8j+8) of the first half and [64+8j, 64+8j+8) of the second half, so
 // every rotate-half pair (x[i], x[i+64]) sits in one lane and each lane moves
 // two 16-byte chunks. The RMS sum is reduced over the 8 lanes of the group.
+// The forward kernels give each group more than one section (see each).
 //
 // These kernels are HBM-bound: per section they read 256 B and write 256 B;
 // cos/sin rows (2 x 256 B per token) and the weights stay in L2/L1.
@@ -14,60 +15,97 @@
 
 namespace aa {
 
-// Forward of one section: rstd over 128 values, y = bf16(x * rstd * w), then
-// optional rotation (norm_rotate), bf16 store.
-template <bool ROTATE>
-__device__ __forceinline__ void norm_section(const bf16* src, bf16* dst, const float* w,
-                                             const float* cos, const float* sin, int64_t pos,
-                                             int j, float eps) {
-  Section x;
-  load_section(src, j, x);
-  float oa[8], ob[8];
-  norm_rotate<ROTATE>(x, w, cos, sin, pos, j, eps, oa, ob);
-  st16_nt(dst + 8 * j, pack8(oa));
-  st16_nt(dst + kHalf + 8 * j, pack8(ob));
-}
+// Section counts are below kMaxSections (the host checks): 2^31 sections of
+// 256 bytes would be 512 GiB, more than one GPU holds, so 32-bit section
+// indices cover every real tensor.
+constexpr uint32_t kMaxSections = 0x7fffff00u;
 
-// qkv [ntok, 3*H*128] -> q, k [ntok, H, 128] (+ v copy). Sections of a token:
-// [0,H) q heads, [H,2H) k heads, [2H,3H) v heads (only when v != nullptr).
+// qkv [ntok, 3*H*128] -> q, k [ntok, H, 128] (+ v copy). A token's qkv row
+// holds its q heads, then its k heads, then its v heads. Each 8-lane group
+// takes one (token, head) pair: the q and k sections of that head (and the v
+// section when copying V), which share the RoPE row of the token's position.
+// All of the group's section loads are issued first, so a lane has four
+// 16-byte loads in flight (six with V). A wave covers 8 consecutive pairs.
 template <bool WITH_V>
-__global__ __launch_bounds__(256) void qkv_norm_rope_fwd_kernel(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) void
+qkv_norm_rope_fwd_kernel(
     const bf16* __restrict__ qkv, bf16* __restrict__ q, bf16* __restrict__ k,
     bf16* __restrict__ v, const float* __restrict__ qw, const float* __restrict__ kw,
-    const float* __restrict__ cos, const float* __restrict__ sin, int64_t ntok, int64_t S,
-    int H, float eps) {
+    const float* __restrict__ cos, const float* __restrict__ sin, uint32_t npair, uint32_t S,
+    uint32_t H, float eps) {
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int j = (int)(gid & 7);
-  const int64_t group = gid >> 3;
-  const int nsec = WITH_V ? 3 * H : 2 * H;
-  const int64_t token = group / nsec;
-  if (token >= ntok) return;
-  const int sec = (int)(group - token * nsec);
-  const int which = sec / H;
-  const int head = sec - which * H;
+  // The last wave's surplus groups compute the last pair and store nothing.
+  const bool valid = (gid >> 3) < (int64_t)npair;
+  const uint32_t pair = valid ? (uint32_t)(gid >> 3) : npair - 1;
+  const uint32_t token = pair / H;
+  const uint32_t head = pair - token * H;
   const int64_t width = (int64_t)H * kHd;
-  const bf16* src = qkv + token * 3 * width + which * width + head * kHd;
-  const int64_t dst_off = token * width + head * kHd;
-  if (WITH_V && which == 2) {
-    st16_nt(v + dst_off + 8 * j, ld16(src + 8 * j));
-    st16_nt(v + dst_off + kHalf + 8 * j, ld16(src + kHalf + 8 * j));
-    return;
+  const bf16* row = qkv + (int64_t)token * 3 * width + head * kHd;
+  RawSection xq, xk, xv;
+  load_raw(row, j, xq);
+  load_raw(row + width, j, xk);
+  if constexpr (WITH_V) load_raw(row + 2 * width, j, xv);
+  float c[8], s[8];
+  load_rot(cos, sin, token % S, j, c, s);
+  // Keeps all loads ahead of the first section's arithmetic.
+  __builtin_amdgcn_sched_barrier(0);
+  const int64_t dst_off = (int64_t)token * width + head * kHd;
+  if constexpr (WITH_V) {
+    if (valid) {
+      st16_nt(v + dst_off + 8 * j, xv.a);
+      st16_nt(v + dst_off + kHalf + 8 * j, xv.b);
+    }
   }
-  const int64_t pos = token % S;
-  norm_section<true>(src, (which == 0 ? q : k) + dst_off, which == 0 ? qw : kw, cos, sin, pos, j,
-                     eps);
+  float oa[8], ob[8];
+  norm_scale(unpack_section(xq), qw, j, eps, oa, ob);
+  rotate_half(oa, ob, c, s);
+  if (valid) {
+    st16_nt(q + dst_off + 8 * j, pack8(oa));
+    st16_nt(q + dst_off + kHalf + 8 * j, pack8(ob));
+  }
+  norm_scale(unpack_section(xk), kw, j, eps, oa, ob);
+  rotate_half(oa, ob, c, s);
+  if (valid) {
+    st16_nt(k + dst_off + 8 * j, pack8(oa));
+    st16_nt(k + dst_off + kHalf + 8 * j, pack8(ob));
+  }
+}
+
+// Sections per 8-lane group in head_norm_fwd_kernel: a lane then has
+// 2 kHnSecs 16-byte loads in flight before its first use. A wave takes
+// 8 kHnSecs consecutive sections, its group r sections r, r + 8, ..., so
+// each pair of load instructions reads 2 KiB of consecutive bytes.
+constexpr int kHnSecs = 2;
+
+// Section index of round i for lane gid.
+__device__ __forceinline__ uint32_t hn_section(int64_t gid, int i) {
+  return (uint32_t)(gid >> 6) * (8 * kHnSecs) + 8 * i + ((uint32_t)(gid >> 3) & 7);
 }
 
 // x [ntok, H*128] -> y [ntok, H, 128].
 __global__ __launch_bounds__(256) void head_norm_fwd_kernel(const bf16* __restrict__ x,
                                                             bf16* __restrict__ y,
                                                             const float* __restrict__ w,
-                                                            int64_t nsec, float eps) {
+                                                            uint32_t nsec, float eps) {
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t sec = gid >> 3;
-  if (sec >= nsec) return;
   const int j = (int)(gid & 7);
-  norm_section<false>(x + sec * kHd, y + sec * kHd, w, nullptr, nullptr, 0, j, eps);
+  RawSection xs[kHnSecs];
+#pragma unroll
+  for (int i = 0; i < kHnSecs; ++i)
+    load_raw(x + (int64_t)min(hn_section(gid, i), nsec - 1) * kHd, j, xs[i]);
+  __builtin_amdgcn_sched_barrier(0);  // all rounds' loads first
+#pragma unroll
+  for (int i = 0; i < kHnSecs; ++i) {
+    const uint32_t sec = hn_section(gid, i);
+    float oa[8], ob[8];
+    norm_scale(unpack_section(xs[i]), w, j, eps, oa, ob);
+    if (sec < nsec) {  // out-of-range rounds computed the clamped last section
+      bf16* dst = y + (int64_t)sec * kHd;
+      st16_nt(dst + 8 * j, pack8(oa));
+      st16_nt(dst + kHalf + 8 * j, pack8(ob));
+    }
+  }
 }
 
 // ------------------------------------------------------------- backward --
@@ -292,18 +330,19 @@ extern "C" int aa_qkv_norm_rope_fwd(const void* qkv, void* q, void* k, void* v,
   if (!aligned16(qkv) || !aligned16(q) || !aligned16(k) || (v && !aligned16(v)) ||
       !aligned16(q_weight) || !aligned16(k_weight) || !aligned16(cos) || !aligned16(sin))
     return fail(AA_EINVAL, "qkv_norm_rope_fwd: pointers must be 16-byte aligned");
-  const int64_t ntok = B * S;
-  const int64_t lanes = ntok * (v ? 3 : 2) * H * 8;
-  const dim3 grid((unsigned)((lanes + 255) / 256));
+  const int64_t npair = B * S * H;
+  if (3 * npair > (int64_t)kMaxSections)
+    return fail(AA_EINVAL, "qkv_norm_rope_fwd: tensor too large");
+  const dim3 grid((unsigned)((npair * 8 + 255) / 256));
   hipStream_t st = (hipStream_t)stream;
   if (v) {
     qkv_norm_rope_fwd_kernel<true><<<grid, 256, 0, st>>>(
-        (const bf16*)qkv, (bf16*)q, (bf16*)k, (bf16*)v, q_weight, k_weight, cos, sin, ntok, S,
-        (int)H, eps);
+        (const bf16*)qkv, (bf16*)q, (bf16*)k, (bf16*)v, q_weight, k_weight, cos, sin,
+        (uint32_t)npair, (uint32_t)S, (uint32_t)H, eps);
   } else {
     qkv_norm_rope_fwd_kernel<false><<<grid, 256, 0, st>>>(
-        (const bf16*)qkv, (bf16*)q, (bf16*)k, nullptr, q_weight, k_weight, cos, sin, ntok, S,
-        (int)H, eps);
+        (const bf16*)qkv, (bf16*)q, (bf16*)k, nullptr, q_weight, k_weight, cos, sin,
+        (uint32_t)npair, (uint32_t)S, (uint32_t)H, eps);
   }
   return check_launch("qkv_norm_rope_fwd");
 }
@@ -317,9 +356,10 @@ extern "C" int aa_head_norm_fwd(const void* x, void* y, const float* weight, int
   if (!aligned16(x) || !aligned16(y) || !aligned16(weight))
     return fail(AA_EINVAL, "head_norm_fwd: pointers must be 16-byte aligned");
   const int64_t nsec = B * S * H;
-  const dim3 grid((unsigned)((nsec * 8 + 255) / 256));
+  if (nsec > (int64_t)kMaxSections) return fail(AA_EINVAL, "head_norm_fwd: tensor too large");
+  const dim3 grid((unsigned)(((nsec + kHnSecs - 1) / kHnSecs * 8 + 255) / 256));
   head_norm_fwd_kernel<<<grid, 256, 0, (hipStream_t)stream>>>((const bf16*)x, (bf16*)y, weight,
-                                                              nsec, eps);
+                                                              (uint32_t)nsec, eps);
   return check_launch("head_norm_fwd");
 }
 
