@@ -88,9 +88,12 @@ def test_workspace_sizes(lib):
     # one 1 KB stats record per 64-query tile, per (batch, head)
     assert lib.aa_attn_bwd_workspace(2, 100, 77, 3, 128) == 2 * 3 * 2 * 1024
     assert lib.aa_attn_bwd_workspace(1, 0, 77, 3, 128) == 0
-    # weight-gradient partials: one [2][128] (or [128]) fp32 record per 8 tokens
-    assert lib.aa_qkv_norm_rope_bwd_workspace(1, 4096, 16, 128) == 512 * 2 * 128 * 4
-    assert lib.aa_head_norm_bwd_workspace(2, 9, 5, 128) == 3 * 128 * 4
+    # weight-gradient partials: one [2][128] fp32 record per block of 64
+    # (token, head) items, one [128] record per 128 items for head_norm
+    assert lib.aa_qkv_norm_rope_bwd_workspace(1, 4096, 16, 128) == 1024 * 2 * 128 * 4
+    assert lib.aa_head_norm_bwd_workspace(2, 9, 5, 128) == 1 * 128 * 4
+    assert lib.aa_head_norm_bwd_workspace(2, 65, 1, 128) == 2 * 128 * 4
+    assert lib.aa_head_norm_bwd_workspace(0, 65, 1, 128) == 0
     # one int32 per 32 context rows per item
     assert lib.aa_context_lengths_workspace(3, 77) == 3 * 3 * 4
     assert lib.aa_context_lengths_workspace(0, 77) == 0

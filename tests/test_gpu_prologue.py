@@ -48,7 +48,9 @@ def test_qkv_norm_rope_grad_variant_copies_v(pkg, dev):
     assert torch.equal(v.detach().float().cpu(), inp["qkv"].view(B, S, 3, H, 128)[:, :, 2])
 
 
-@pytest.mark.parametrize("B,S,H", [(1, 4096, 16), (2, 50, 3)])
+# Blocks of 64 (token, head) items: 4 whole tokens (H 16), 64 (H 1), blocks
+# that straddle tokens (H 3, H 48), and a partial last block.
+@pytest.mark.parametrize("B,S,H", [(1, 4096, 16), (2, 50, 3), (1, 333, 1), (1, 77, 48)])
 def test_qkv_norm_rope_backward(pkg, dev, B, S, H):
     eps = 1e-6
     inp = _inputs(B, S, H, seed=200 + S)
@@ -74,8 +76,8 @@ def test_qkv_norm_rope_backward(pkg, dev, B, S, H):
 def test_qkv_norm_rope_backward_deterministic_c_abi(pkg, dev, B, S, H):
     """Two calls through the C ABI on one (uninitialised) workspace give the
     op's results bit for bit: the weight-gradient reduction sums in a fixed
-    order whatever the partials' layout of blocks (512, 125 and 13 chunks of 8
-    tokens)."""
+    order whatever the number of partial records (1024, 63 and 5 blocks of 64
+    (token, head) items)."""
     import ctypes
 
     L = pkg._lib
@@ -105,7 +107,7 @@ def test_qkv_norm_rope_backward_deterministic_c_abi(pkg, dev, B, S, H):
         assert torch.equal(dqw, expected[1]) and torch.equal(dkw, expected[2]), f"call {call}: weight grads"
 
 
-@pytest.mark.parametrize("B,S,H", [(2, 4096, 16), (1, 9, 5)])
+@pytest.mark.parametrize("B,S,H", [(2, 4096, 16), (1, 9, 5), (1, 300, 1)])
 def test_head_norm_forward_backward(pkg, dev, B, S, H):
     eps = 1e-6
     g = torch.Generator().manual_seed(300 + S)

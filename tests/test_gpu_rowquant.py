@@ -32,6 +32,11 @@ def _rows(B, S, K, seed, spread=False):
         (3, 5, 8, False),  # one chunk per row
         (2, 40, 2048, True),
         (1, 7, 1000, True),  # K not a multiple of 256 * 8
+        # Each (units per lane, values per unit) instantiation: 16-value units
+        # when K % 16 == 0, 8-value units otherwise.
+        (1, 9, 4096, True),
+        (1, 5, 3000, False),
+        (1, 3, 8184, True),
     ],
 )
 def test_rowquant_bit_exact(pkg, fp8, B, S, K, spread):
@@ -46,8 +51,9 @@ def test_rowquant_bit_exact(pkg, fp8, B, S, K, spread):
     assert torch.equal(qb, eb), f"{(qb != eb).sum().item()} bytes differ"
 
 
-def test_rowquant_gelu(pkg, fp8):
-    B, S, K = 2, 48, 8192
+@pytest.mark.parametrize("K", [8192, 1000])
+def test_rowquant_gelu(pkg, fp8, K):
+    B, S = 2, 48
     x = _rows(B, S, K, seed=9) * 3
     q, s = fp8.rowquant(x.to("cuda:0"), gelu=True)
     torch.cuda.synchronize()
