@@ -60,7 +60,10 @@
 //   per score. m is only raised when a tile's max exceeds it by more than
 //   8/c (8 in log2 units), so p <= 256 and the O/l rescale (a pass over the
 //   128 accumulator registers) runs only a few times per row. The row sum is
-//   taken over the bf16-rounded P that feeds the MFMA, with v_dot2c_f32_bf16.
+//   taken over the bf16-rounded P that feeds the MFMA, on the matrix pipe: a
+//   v_mfma_f32_16x16x32_bf16 of each P operand against a 0/1 selector (see
+//   FwdWave::setup), 8 small MFMAs per tile in place of 32 v_dot2c_f32_bf16,
+//   each of which held the matrix pipe for about half an MFMA.
 #include <algorithm>
 #include <atomic>
 #include <cmath>

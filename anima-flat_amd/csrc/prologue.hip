@@ -309,46 +309,53 @@ __global__ __launch_bounds__(kBwdThreads) void head_norm_bwd_kernel(NormBwdParam
 }
 
 // Weight-gradient reduction of partial[nrow][n] (n = 128 or 256 outputs) in
-// one launch, in a fixed order. Block b owns outputs 4 b .. 4 b + 3, one
-// 16-byte column of every partial row: thread t sums rows t, t + 256, ...
-// (a batch's loads issued together, then added in order) and the 256 thread
-// sums meet in a fixed pairwise tree through LDS. The launch is bound by
-// latency, not bytes: ~4.5 us for 1 MB of partials with 8 blocks reading
-// whole 128-byte lines or 64 blocks reading 16-byte columns alike. (Folding this into
-// the norm kernel's tail, the last block of each group of chunks adding
-// behind a device-scope atomic counter, measured 105 us instead of ~30 for
-// the whole backward: on the 8-XCD MI355X a device-scope release fence
-// writes back the XCD's L2, once per block.)
-constexpr int kRedThreads = 256;
-constexpr int kRedCols = 4;
+// one launch, in a fixed order. Block b owns outputs 32 b .. 32 b + 31, one
+// 128-byte line of every partial row: 8 lanes read a row's line as 16-byte
+// loads (so the launch fetches each partial byte once), 128 row groups take
+// rows r, r + 128, ... (a batch's loads issued together, then added in
+// order), and the 128 group sums meet in a fixed pairwise tree through LDS.
+// The launch is bound by latency, not bytes: ~4.1-4.7 us for the 1 MB of
+// config 5's partials, the same with 64 blocks reading 16-byte columns
+// (which fetch each line 8 times). (Folding this into the norm kernel's
+// tail, the last block of each group of chunks adding behind a device-scope
+// atomic counter, measured 105 us instead of ~30 for the whole backward: on
+// the 8-XCD MI355X a device-scope release fence writes back the XCD's L2,
+// once per block.)
+constexpr int kRedThreads = 1024;
+constexpr int kRedRowGroups = kRedThreads / 8;
+constexpr int kRedCols = 32;
 __global__ __launch_bounds__(kRedThreads) void reduce_partials_kernel(
     const float* __restrict__ partial, uint32_t nrow, int n, float* __restrict__ out0,
     float* __restrict__ out1) {
-  constexpr int kBatch = 4;
-  __shared__ f32x4 red[kRedThreads];
-  const int tid = threadIdx.x;
-  const int col = blockIdx.x * kRedCols;
+  constexpr int kBatch = 8;
+  __shared__ f32x4 red[kRedRowGroups][8];
+  const int l8 = threadIdx.x & 7;
+  const int rg = threadIdx.x >> 3;
+  const int col = blockIdx.x * kRedCols + 4 * l8;
   f32x4 s = {0.f, 0.f, 0.f, 0.f};
-  uint32_t r = tid;
-  for (; r + (uint32_t)kRedThreads * (kBatch - 1) < nrow; r += kRedThreads * kBatch) {
+  uint32_t r = rg;
+  for (; r + (uint32_t)kRedRowGroups * (kBatch - 1) < nrow; r += kRedRowGroups * kBatch) {
     f32x4 t[kBatch];
 #pragma unroll
-    for (int i = 0; i < kBatch; ++i) t[i] = ldf4(partial + (int64_t)(r + kRedThreads * i) * n + col);
+    for (int i = 0; i < kBatch; ++i)
+      t[i] = ldf4(partial + (int64_t)(r + kRedRowGroups * i) * n + col);
 #pragma unroll
     for (int i = 0; i < kBatch; ++i) s += t[i];
   }
-  for (; r < nrow; r += kRedThreads) s += ldf4(partial + (int64_t)r * n + col);
-  red[tid] = s;
+  for (; r < nrow; r += kRedRowGroups) s += ldf4(partial + (int64_t)r * n + col);
+  red[rg][l8] = s;
   __syncthreads();
 #pragma unroll
-  for (int w = kRedThreads / 2; w > 0; w >>= 1) {
-    if (tid < w) red[tid] += red[tid + w];
+  for (int w = kRedRowGroups / 2; w > 0; w >>= 1) {
+    if (rg < w) red[rg][l8] += red[rg + w][l8];
     __syncthreads();
   }
-  if (tid < kRedCols) {
-    const int o = col + tid;
-    if (o < kHd) out0[o] = red[0][tid];
-    else out1[o - kHd] = red[0][tid];
+  if (threadIdx.x < kRedCols) {
+    const int c = threadIdx.x;
+    const int o = blockIdx.x * kRedCols + c;
+    const float t = red[0][c / 4][c % 4];
+    if (o < kHd) out0[o] = t;
+    else out1[o - kHd] = t;
   }
 }
 
