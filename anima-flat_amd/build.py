@@ -24,7 +24,7 @@ LIB_NAME = "libanima_attn.so"
 LIB_PATH = HERE / LIB_NAME
 SOURCES = (
     "abi.hip", "prologue.hip", "ctx_scale.hip", "context.hip", "rowquant.hip", "attn_fwd.hip",
-    "attn_fwd_pp.hip", "attn_fwd_d384.hip", "attn_bwd.hip", "qkv_proj.hip",
+    "attn_fwd_pp.hip", "attn_fwd_d384.hip", "attn_bwd.hip", "attn_bwd_dkdv.hip", "qkv_proj.hip",
 )
 ARCH = "gfx950"
 
@@ -44,13 +44,14 @@ DEVICE_FLAGS = [
 
 RESOURCE_REMARK = "-Rpass-analysis=kernel-resource-usage"
 
-# Per-source extra flags. attn_fwd.hip runs one wave per SIMD, where the
-# compiler would otherwise give every MFMA accumulator the AGPR file; its
-# score accumulators must be VGPRs (the softmax reads them), so the builtin
-# MFMAs are compiled in the VGPR form and the output accumulators are pinned to
-# AGPRs through inline asm.
+# Per-source extra flags. attn_fwd.hip and attn_bwd_dkdv.hip run one wave per
+# SIMD, where the compiler would otherwise give every MFMA accumulator the
+# AGPR file; their score accumulators must be VGPRs (the VALU reads them), so
+# the builtin MFMAs are compiled in the VGPR form and the output accumulators
+# are pinned to AGPRs through inline asm.
 SOURCE_FLAGS: dict[str, list[str]] = {
     "attn_fwd.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+    "attn_bwd_dkdv.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
 }
 
 

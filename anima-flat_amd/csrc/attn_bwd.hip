@@ -29,41 +29,17 @@
 // accumulator row order, so the bf16-rounded accumulators are the B operands
 // as they are.
 #include <algorithm>
+#include <cstdlib>
+#include <string>
 
+#include "attn_bwd.h"
 #include "tile_io.h"
 
 namespace aa {
 
 namespace bwd {
 
-constexpr int kD = 128;
-constexpr int kT = kTileRows;  // rows (queries or keys) per streamed tile
-constexpr int kStat = 256;     // floats per 64-query stats record: lse2[64], -D[64], zero pad
-
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
-
-struct Params {
-  const bf16* dout;
-  const bf16* q;
-  const bf16* k;
-  const bf16* v;
-  const bf16* o;
-  const float* lse;
-  bf16* dq;
-  bf16* dk;
-  bf16* dv;
-  int64_t s_do[3], s_q[3], s_k[3], s_v[3], s_o[3], s_dq[3], s_dk[3], s_dv[3];
-  float* stats;  // [B][H][ntq][kStat]
-  // Query split of dkdv_kernel (see dkdv_split): with nsplit > 1, workgroup
-  // (split, b, h, key block) covers query tiles split * ceil(ntq / nsplit) ..
-  // and writes its fp32 dV^T / dK^T accumulators to part (layout at
-  // dkdv_combine_kernel), which the combine pass sums in a fixed order.
-  float* part;
-  int nsplit;
-  int H, Sq, Sk, ntq, ntk;
-  float c;      // scale * log2(e)
-  float scale;  // softmax scale
-};
 
 // ------------------------------------------------------------ dK, dV --
 
@@ -90,8 +66,8 @@ struct Params {
 // previous tile) are pairs of ds_read_b64_tr_b16 transposed reads of the same
 // tiles. The B waves DMA tile t+2 at the start of X_B(t-1) (phase 2t); it is
 // complete at the end of phase 2t+3.
-constexpr int kKeysPerWg = 128;
 constexpr int kDkWaves = 8;
+static_assert(kDkWaves == kDkParts, "one partial record per wave");
 constexpr int kDkQueue = 8;   // A operands in flight per wave
 constexpr int kDkStages = 4;  // query tiles in the LDS ring
 
@@ -307,12 +283,14 @@ void dkdv_kernel(Params p, int nkblk, int total_blocks) {
   else stage_rows_out(p.dk + b * p.s_dk[0] + h * p.s_dk[2], p.s_dk[1], key0, p.Sk, lane, ostage);
 }
 
-// Sums the query-split partials of dkdv_kernel in split order and writes dV
-// and dK (times the softmax scale) as bf16. A workgroup's partial holds, per
-// wave w, float4 j of lane l at ((w * 16 + j) * 64 + l): accumulator block
-// dt = j / 4, registers 4 (j % 4) .. + 3, i.e. key 32 (w % 4) + l % 32 of the
-// key block and head-dim 32 dt + 8 (j % 4) + 4 (l / 32) .. + 3; waves 0-3
-// hold dV^T, 4-7 dK^T. One thread per (key, 8 consecutive head-dims): the
+// Sums the query-split partials of either dK/dV kernel in split order and
+// writes dV and dK (times the softmax scale) as bf16. A workgroup's partial
+// holds, per record w, float4 j of lane l at ((w * 16 + j) * 64 + l):
+// accumulator block dt = j / 4, registers 4 (j % 4) .. + 3, i.e. key
+// 32 (w % 4) + l % 32 of the key block and head-dim 32 dt + 8 (j % 4) +
+// 4 (l / 32) .. + 3; records 0-3 hold dV^T, 4-7 dK^T (the waves of
+// dkdv_kernel; both accumulators of each wave of the one-wave kernel). One
+// thread per (key, 8 consecutive head-dims): the
 // float4s of lanes l and l + 32 of every split, all loaded before the sums,
 // and one 16-byte store (8-byte stores of one lane's half took 11.7 us for
 // B=2, 512 keys, 16 heads, 2 splits).
@@ -328,8 +306,8 @@ __global__ __launch_bounds__(256) void dkdv_combine_kernel(Params p, int nkblk, 
   const int b = bh / p.H, h = bh - b * p.H;
   const int key = kblk * kKeysPerWg + (wave & 3) * 32 + li;
   if (key >= p.Sk) return;
-  const f32x4* src = reinterpret_cast<const f32x4*>(p.part) + (((int64_t)rest * kDkWaves + wave) * 16 + j) * 64 + li;
-  const int64_t split_stride = (int64_t)per_split * kDkWaves * 16 * 64;
+  const f32x4* src = reinterpret_cast<const f32x4*>(p.part) + (((int64_t)rest * kDkParts + wave) * 16 + j) * 64 + li;
+  const int64_t split_stride = (int64_t)per_split * kDkParts * 16 * 64;
   f32x4 v[kMaxDkSplit][2];
 #pragma unroll
   for (int s = 0; s < kMaxDkSplit; ++s) {
@@ -622,9 +600,23 @@ static WsLayout ws_layout(int64_t B, int64_t Sq, int64_t Sk, int64_t H) {
   w.part = w.stats + (size_t)(B * H * ntq) * kStat * sizeof(float);
   const int64_t blocks = B * H * ((Sk + kKeysPerWg - 1) / kKeysPerWg);
   const size_t part_bytes =
-      w.nsplit > 1 ? (size_t)w.nsplit * blocks * kDkWaves * 64 * 64 * sizeof(float) : 0;
+      w.nsplit > 1 ? (size_t)w.nsplit * blocks * kDkParts * 64 * 64 * sizeof(float) : 0;
   w.total = w.part + part_bytes;
   return w;
+}
+
+// Which dK/dV kernel runs: the one-wave-per-SIMD kernel of attn_bwd_dkdv.hip
+// (1, the default) or the two-role kernel above (0). AA_DKDV_KERNEL=1w|2role
+// forces one (the GPU tests run both on every shape); -1 for another value.
+static int dkdv_kernel_choice() {
+  const char* e = std::getenv("AA_DKDV_KERNEL");
+  if (e && *e) {
+    const std::string v = e;
+    if (v == "2role") return 0;
+    if (v == "1w") return 1;
+    return -1;
+  }
+  return 1;
 }
 
 }  // namespace bwd
@@ -665,6 +657,8 @@ extern "C" int aa_attn_bwd(const aa_attn_bwd_args* a, void* workspace, size_t wo
     if (s[1] < 0 || s[1] >= (1 << 24))
       return fail(AA_EUNSUPPORTED, "attn_bwd: q / dout / k / v sequence strides must be in [0, 2^24) elements");
   if (!(a->softmax_scale > 0.f)) return fail(AA_EINVAL, "attn_bwd: softmax_scale must be > 0");
+  const int dkdv_which = bwd::dkdv_kernel_choice();
+  if (dkdv_which < 0) return fail(AA_EINVAL, "AA_DKDV_KERNEL must be 1w or 2role");
   const bwd::WsLayout wl = bwd::ws_layout(a->B, a->Sq, a->Sk, a->H);
   const size_t need = aa_attn_bwd_workspace(a->B, a->Sq, a->Sk, a->H, a->hd);
   if (need > 0 && (!workspace || workspace_bytes < need))
@@ -718,10 +712,11 @@ extern "C" int aa_attn_bwd(const aa_attn_bwd_args* a, void* workspace, size_t wo
     const int nkblk = (int)((a->Sk + bwd::kKeysPerWg - 1) / bwd::kKeysPerWg);
     const int per_split = (int)(BH * nkblk);
     const int total = per_split * p.nsplit;
-    bwd::dkdv_kernel<<<dim3((unsigned)total), bwd::kDkWaves * 64, 0, st>>>(p, nkblk, total);
+    if (dkdv_which == 1) bwd::launch_dkdv1w(p, nkblk, total, st);
+    else bwd::dkdv_kernel<<<dim3((unsigned)total), bwd::kDkWaves * 64, 0, st>>>(p, nkblk, total);
     if (int rc = check_launch("attn_bwd dkdv")) return rc;
     if (p.nsplit > 1) {
-      const int64_t threads = (int64_t)per_split * bwd::kDkWaves * 16 * 32;
+      const int64_t threads = (int64_t)per_split * bwd::kDkParts * 16 * 32;
       bwd::dkdv_combine_kernel<<<dim3((unsigned)(threads / 256)), 256, 0, st>>>(p, nkblk, per_split);
       if (int rc = check_launch("attn_bwd dkdv combine")) return rc;
     }

@@ -397,6 +397,45 @@ def test_both_forward_kernels(pkg, monkeypatch, kernel, B, Sq, Sk, H, lens):
     parity(lse, el, **LSE_TOL, name=f"lse {tag}")
 
 
+@pytest.mark.parametrize("kernel", ["1w", "2role"])
+@pytest.mark.parametrize(
+    "B,Sq,Sk,H",
+    [
+        (2, 100, 77, 3),  # partial query and key tiles, keys past Sk in every wave
+        (1, 64, 300, 1),  # one query tile
+        (1, 2048, 256, 4),  # 8 key blocks: the query range split over 4 workgroups
+        (1, 1000, 300, 2),  # split with a partial last query tile
+        (1, 1024, 1024, 4),
+    ],
+)
+def test_both_dkdv_kernels(pkg, monkeypatch, kernel, B, Sq, Sk, H):
+    """aa_attn_bwd runs the one-wave-per-SIMD dK/dV kernel unless AA_DKDV_KERNEL=2role
+    picks the two-role one; each is held to the oracle on every shape, with and
+    without the query split and its combine pass."""
+    q, k, v = _qkv(B, Sq, Sk, H, seed=9200 + Sq + Sk + H)
+    g = torch.Generator().manual_seed(9201)
+    dout = ref.bf16_normal((B, Sq, H, 128), g)
+    qd, kd, vd = _gpu(q, k, v)
+    out, lse = torch.ops.anima_flat.fa_fwd(qd, kd, vd)
+    monkeypatch.setenv("AA_DKDV_KERNEL", kernel)
+    dqg, dkg, dvg = torch.ops.anima_flat.fa_bwd(dout.to("cuda", BF), qd, kd, vd, out, lse)
+    torch.cuda.synchronize()
+    monkeypatch.delenv("AA_DKDV_KERNEL")
+    dq, dk, dv = ref.attention_backward(q, k, v, dout)
+    tag = f"{kernel} B{B} Sq{Sq} Sk{Sk} H{H}"
+    parity(dqg, dq, name=f"dq {tag}")
+    parity(dkg, dk, name=f"dk {tag}")
+    parity(dvg, dv, name=f"dv {tag}")
+
+
+def test_dkdv_kernel_env_rejects_unknown_value(pkg, monkeypatch):
+    q, k, v = _gpu(*_qkv(1, 64, 64, 1, seed=9300))
+    out, lse = torch.ops.anima_flat.fa_fwd(q, k, v)
+    monkeypatch.setenv("AA_DKDV_KERNEL", "zz")
+    with pytest.raises(ValueError, match="AA_DKDV_KERNEL"):
+        torch.ops.anima_flat.fa_bwd(torch.ones_like(q), q, k, v, out, lse)
+
+
 def test_forward_kernel_env_rejects_unknown_value(pkg, monkeypatch):
     q, k, v = _gpu(*_qkv(1, 64, 64, 1, seed=9100))
     monkeypatch.setenv("AA_FWD_KERNEL", "zz")
