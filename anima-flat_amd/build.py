@@ -27,6 +27,10 @@ SOURCES = (
     "attn_fwd_pp.hip", "attn_fwd_d384.hip", "attn_bwd.hip", "attn_bwd_dkdv.hip", "qkv_proj.hip",
 )
 ARCH = "gfx950"
+# The measurement's MFMA-rate calibration (bench.py), a library of its own so
+# that the attention library holds only the path's entry points.
+CALIB_SOURCE = "calib_mfma.hip"
+CALIB_LIB_PATH = HERE / "libanima_calib.so"
 
 # Packed fp32 VALU forms are disabled for all device code: the compiler then
 # emits only scalar v_fma_f32/v_mul_f32 for float arithmetic.
@@ -112,15 +116,17 @@ def _run(cmd: list[str]) -> None:
 
 
 def build(verbose: bool = False) -> Path:
-    """Compile every source and link libanima_attn.so; returns the library path."""
+    """Compile every source, link libanima_attn.so and the calibration library
+    libanima_calib.so; returns the attention library's path."""
     cc = hipcc()
     SGPR_SPILL_WARNINGS.clear()
     BUILD.mkdir(exist_ok=True)
     objs = []
     cmds = []
-    for src in SOURCES:
+    for src in SOURCES + (CALIB_SOURCE,):
         obj = BUILD / (Path(src).stem + ".o")
-        objs.append(str(obj))
+        if src != CALIB_SOURCE:
+            objs.append(str(obj))
         cmds.append([cc, *DEVICE_FLAGS, *SOURCE_FLAGS.get(src, []), RESOURCE_REMARK, "-c",
                      str(CSRC / src), "-o", str(obj)])
     workers = max(1, min(len(cmds), os.cpu_count() or 1, 8))
@@ -134,6 +140,10 @@ def build(verbose: bool = False) -> Path:
         print(" ".join(link), flush=True)
     _run(link)
     os.replace(tmp, LIB_PATH)
+    ctmp = CALIB_LIB_PATH.with_suffix(".so.tmp")
+    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(ctmp),
+          str(BUILD / (Path(CALIB_SOURCE).stem + ".o"))])
+    os.replace(ctmp, CALIB_LIB_PATH)
     return LIB_PATH
 
 

@@ -20,6 +20,11 @@ HBM GB/s, masked cross-attention (config 3), forward+backward (config 5),
 the 28-layer attention time of one CFG denoiser step at 1024x1024, and the
 VAE decoder's head_dim-384 attention at 1024x1024.
 
+`mfma_sustained`: the rate at which this GPU sustains back-to-back
+v_mfma_f32_32x32x16_bf16 on register operands (no memory traffic) of three
+distributions, all CUs (csrc/calib_mfma.hip, libanima_calib.so): context for
+`roofline.frac`, which stays against the published dense peak.
+
 `cpu_baseline`: the reference's non-FA4 path, torch SDPA (math backend) in
 fp32 on the host CPU, on a bounded sample of config 2 (a subset of heads),
 scaled to TFLOP/s.
@@ -250,6 +255,34 @@ def prologue_qkv(pkg, B, S, H, seed, dev):
     return t
 
 
+CALIB_DISTS = ((0, "N(0,1)"), (1, "U[0,1)"), (2, "zero"))
+
+
+def mfma_sustained(achieved: float) -> dict:
+    """Sustained MFMA-only rate per operand distribution (libanima_calib.so:
+    aa_calib_mfma, 20000 iterations of 8 MFMAs per wave, best of 3 launches),
+    and the headline kernel's achieved rate as a fraction of the N(0,1) one."""
+    path = ROOT / "anima-flat_amd" / "libanima_calib.so"
+    if not path.exists():
+        raise RuntimeError(f"{path} is missing: run __graft_entry__.build() first")
+    lib = ctypes.CDLL(str(path))
+    lib.aa_calib_mfma.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                  ctypes.POINTER(ctypes.c_float), ctypes.c_void_p]
+    lib.aa_calib_mfma.restype = ctypes.c_int
+    stream = torch.cuda.current_stream().cuda_stream
+    out = {"what": "back-to-back v_mfma_f32_32x32x16_bf16 on register operands, one wave per SIMD "
+                   "on every CU, no memory traffic (csrc/calib_mfma.hip)",
+           "unit": "TFLOP/s"}
+    for dist, name in CALIB_DISTS:
+        r = ctypes.c_float(0.0)
+        if lib.aa_calib_mfma(dist, 20000, 3, ctypes.byref(r), stream) != 0:
+            raise RuntimeError(f"aa_calib_mfma({dist}) failed")
+        out[name] = round(r.value, 1)
+    out["frac_of_peak"] = {name: round(out[name] / PEAK_BF16_TFLOPS, 4) for _, name in CALIB_DISTS}
+    out["kernel_frac_of_N(0,1)"] = round(achieved / out["N(0,1)"], 4)
+    return out
+
+
 def cpu_baseline(S=4096, H=16, d=128, budget_s=12.0):
     """SDPA math fp32 on the CPU over a subset of config 2's heads."""
     from oracle import attn_oracle as ref
@@ -378,6 +411,8 @@ def main() -> int:
             "kernel_us": round(attn_ms * 1e3, 2),
         },
     }
+
+    result["mfma_sustained"] = mfma_sustained(achieved)
 
     if not args.no_extras:
         extras = {}
