@@ -15,7 +15,10 @@
 //    Each query's lse * log2(e) and -D (D = rowsum(dO o O), from the dO^T
 //    operands it holds and one read of O) it computes itself and writes to a
 //    1 KB stats record per 64 queries for the second kernel.
-// 2. dkdv_kernel: 8 waves, 128 keys per workgroup (32 per wave pair, split
+// 2. a dK/dV kernel: by default dkdv1w_kernel (attn_bwd_dkdv.hip: one wave
+//    per SIMD doing both roles below for its 32 keys, slot-pinned), or with
+//    AA_DKDV_KERNEL=2role this file's dkdv_kernel, described here:
+//    8 waves, 128 keys per workgroup (32 per wave pair, split
 //    by role, the roles one phase apart, at the kernel); streams 64-query
 //    tiles (Q rows, dO rows, stats: 33 KB) into LDS by DMA and reads Q^T and
 //    dO^T from the same rows with transposed LDS reads. Keys are the
