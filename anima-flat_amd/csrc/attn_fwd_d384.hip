@@ -33,9 +33,14 @@
 // K/V staging: a 3-stage LDS ring of 48 KB stages (K and V of 32 keys as
 //   three 32-row x 128 sub-tiles each: K in the row-tile format, V in the
 //   swizzled one, tile_io.h), filled by DMA (global_load_lds_dwordx4). K of
-//   tile t+3 and V of tile t+2 are issued during tile t's phase 1, one DMA
-//   instruction per MFMA slot, so each half has two tiles of lead time;
-//   waves 0-1 move K, waves 2-3 move V.
+//   tile t+3 and V of tile t+2 are issued during tile t, one DMA instruction
+//   every four slots of both phases, so each half has two tiles of lead time;
+//   waves 0-1 move K, waves 2-3 move V. A DMA instruction holds its wave
+//   while the CU's load path is busy: with all 12 of a tile issued in
+//   consecutive slots of phase 1 (the four waves at once), phase 1 took
+//   ~2460 cycles for its 24 MFMAs against ~1150 for phase 2's; spread over
+//   both phases, 434 -> 403 us at 16384 tokens (staggering the four waves'
+//   slots instead was slower, 505 us).
 #include <algorithm>
 #include <cmath>
 #include <string>
@@ -264,7 +269,7 @@ struct Wave {
         sn = mfma32(q[op % kPf], qreg[op], op == 0 ? f32x16{} : sn);
       }
       if constexpr (QK && i < 24) q[i % kPf] = this->template k_op<i>(kb);
-      if constexpr (QK && i >= 2 && i < 14) job.template issue<i - 2>();
+      if constexpr (QK && i % 4 == 2 && i / 4 < kDmaPerTile / 2) job.template issue<i / 4>();
       // P: one score per slot for slots 0-15, packed and summed in pairs.
       if constexpr (i < 16) {
         const float e = fast_exp2(fmaf(s[i], c, -mc));
@@ -290,7 +295,7 @@ struct Wave {
   // Phase 2: O^T += V^T P^T of the current tile (vst) with the row max of the
   // next tile sn (when MAX) in the first slots.
   template <bool MAX>
-  __device__ __forceinline__ void phase2(const bf16* vst) {
+  __device__ __forceinline__ void phase2(const bf16* vst, const DmaJob& job) {
     bf16x8 q[kPf];
     float ma = 0.f, mb = 0.f;
     uint32_t vb0, vb1;
@@ -303,6 +308,7 @@ struct Wave {
         mfma_o(o[db], q[op % kPf], pb[c4]);
       }
       if constexpr (i < 24) q[i % kPf] = this->template v_op<i>(vb0, vb1);
+      if constexpr (i % 4 == 2 && i / 4 < kDmaPerTile / 2) job.template issue<kDmaPerTile / 2 + i / 4>();
       if constexpr (MAX) {
         if constexpr (i == kPf) {
           ma = max3f(sn[0], sn[1], sn[2]);
@@ -454,7 +460,7 @@ void attn_fwd_d384_kernel(Params p) {
       const bool more = t + 1 < n;
       const int kbn = (t0 + t + 1) * kBN;
       if (more && kbn + kBN > it.klen) w.mask(w.sn, kbn, it.klen);
-      w.phase2<true>(stage(t) + kChunks * kSub);
+      w.phase2<true>(stage(t) + kChunks * kSub, job);
       if (more) w.update_max();
       w.s = w.sn;
     }
