@@ -320,9 +320,10 @@ enum SegMode { kCopy = 0, kNorm = 1, kNormRope = 2 };
 // Tile shape for ntok tokens x nsec sections: 0 = TileA, 1 = TileB, 2 =
 // TileC, the one with the least time on the busiest CU: whole rounds of
 // workgroups over the chip (TileC runs two per CU) times the time of one
-// round. Round times measured on MI355X at K = 2048 (graph-timed): A 60 us,
-// B 95 us, C 36.5 us (two workgroups) -> weights 1.93, 3.07, 2 x 0.59. Ties go
-// to the lower index. The environment variable AA_PROJ_TILE = a, b or c
+// round. Round times measured on MI355X at K = 2048 (graph-timed): A 62-66 us,
+// B 87-97 us, C 40 us (two workgroups) -> weights 1.93, 2.85, 2 x 0.62. With
+// them the QKV projection at B = 2 takes two rounds of B (193.5 us) rather
+// than three of A (198.3 us, A/B on one box). Ties go to the lower index. The environment variable AA_PROJ_TILE = a, b or c
 // forces a shape (all give identical results); any other value is an error
 // (-1).
 static int pick_tile(int64_t ntok, int64_t nsec) {
@@ -335,8 +336,8 @@ static int pick_tile(int64_t ntok, int64_t nsec) {
     int64_t mt, ns, per_cu;
     double weight;  // time of one round, per workgroup on a CU
   } shapes[3] = {{TileA::kMT, TileA::kNS, 1, 1.93},
-                 {TileB::kMT, TileB::kNS, 1, 3.07},
-                 {TileC::kMT, TileC::kNS, 2, 0.59}};
+                 {TileB::kMT, TileB::kNS, 1, 2.85},
+                 {TileC::kMT, TileC::kNS, 2, 0.62}};
   int best = 0;
   double best_cost = 0;
   for (int i = 0; i < 3; ++i) {
