@@ -75,6 +75,13 @@ __device__ __forceinline__ float max3f(float a, float b, float c) {
   return r;
 }
 
+// max(a, |b|, |c|) in one v_max3_f32 (a is a running max of magnitudes).
+__device__ __forceinline__ float max3abs(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, |%2|, |%3|" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
 __device__ __forceinline__ float max2f(float a, float b) {
   float r;
   asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));

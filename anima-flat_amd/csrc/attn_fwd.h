@@ -63,18 +63,22 @@ __device__ __forceinline__ Item decode_item(const FwdParams& p, int it) {
 // would mix items of every batch into each round, and with per-batch key
 // lengths (seqused) every round would then last as long as its longest item.
 // Blocks past full_blocks take key range `split` of a split item.
-__device__ __forceinline__ void block_item(const FwdParams& p, int& item_idx, int& split) {
+__device__ __forceinline__ void block_item(const FwdParams& p, int blk, int& item_idx, int& split) {
   split = -1;
-  if ((int)blockIdx.x < p.full_blocks) {
-    const int r = (int)blockIdx.x / p.round_blocks;
-    const int j = (int)blockIdx.x - r * p.round_blocks;
+  if (blk < p.full_blocks) {
+    const int r = blk / p.round_blocks;
+    const int j = blk - r * p.round_blocks;
     const int in_round = min(p.round_blocks, p.full_blocks - r * p.round_blocks);
     item_idx = r * p.round_blocks + xcd_remap(j, in_round);
   } else {
-    const int j = blockIdx.x - p.full_blocks;
+    const int j = blk - p.full_blocks;
     item_idx = p.full_blocks + j / p.nsplit;
     split = j - (j / p.nsplit) * p.nsplit;
   }
+}
+
+__device__ __forceinline__ void block_item(const FwdParams& p, int& item_idx, int& split) {
+  block_item(p, (int)blockIdx.x, item_idx, split);
 }
 
 // Launches the two-group kernel of attn_fwd_pp.hip over `blocks` workgroups.

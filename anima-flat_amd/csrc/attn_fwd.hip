@@ -30,10 +30,10 @@
 // Slot schedule: a tile is 64 slots of one MFMA each; the other work of the
 //   tile is dealt to fixed slots and held there by sched_barrier:
 //     slots  0-31: S^T of tile t+1 (QK)     | P of tile t (fma, exp, bf16, sums)
-//     slots 32-63: O^T += V^T P^T of tile t | the rest of P, then the row max
-//                                             of tile t+1
-//   then the (rare) lazy rescale when tile t+1 raised a row max. The K/V DMA of
-//   tile t+3 is issued one instruction per slot in the first half.
+//     slots 32-63: O^T += V^T P^T of tile t | the rest of P (in the fix-up
+//                                             form: then the row max of tile
+//                                             t+1, and the rare lazy rescale)
+//   The K/V DMA of tile t+3 is issued one instruction per 4 slots.
 //
 // K/V staging (tile_io.h): K and V rows are copied HBM -> LDS by DMA
 //   (global_load_lds_dwordx4) into line tiles, blocks of 8 rows x 64 d that
@@ -54,12 +54,15 @@
 //   keys, the V^T operand only has to list its keys in the same order, which
 //   the transposed reads do by addressing those rows.
 //
-// Online softmax with lazy rescaling
-//   The running max m is tracked on raw scores s = q.k; probabilities are
-//   p = exp2(s*c - m*c) with c = scale * log2(e), one FMA and one v_exp_f32
-//   per score. m is only raised when a tile's max exceeds it by more than
-//   8/c (8 in log2 units), so p <= 256 and the O/l rescale (a pass over the
-//   128 accumulator registers) runs only a few times per row. The row sum is
+// Softmax: first-tile max, fix-up with a running max
+//   Probabilities are p = exp2(s*c - m*c) on raw scores s = q.k with
+//   c = scale * log2(e), one FMA and one v_exp_f32 per score. m is the row
+//   max of the range's first tile, kept for the whole range (see
+//   attn_fwd_fixup_kernel for the rows where that leaves the exponent range).
+//   The fix-up form tracks the running max with lazy rescaling: m is only
+//   raised when a tile's max exceeds it by more than 8/c (8 in log2 units),
+//   so p <= 256 and the O/l rescale (a pass over the 128 accumulator
+//   registers) runs only a few times per row. The row sum is
 //   taken over the bf16-rounded P that feeds the MFMA, on the matrix pipe: a
 //   v_mfma_f32_16x16x32_bf16 of each P operand against a 0/1 selector (see
 //   FwdWave::setup), 8 small MFMAs per tile in place of 32 v_dot2c_f32_bf16,
@@ -383,9 +386,10 @@ struct FwdWave {
 
   // One tile t of the slot schedule. S^T of tile t is in buffer SB; with
   // NEXT, S^T of tile t+1 (its K one ring stage, dstage bytes, past tile t's)
-  // goes to buffer 1 - SB and its row max to mt (masked first when its keys
-  // end inside it: mask_next). The DMA job is issued in its slots.
-  template <int SB, bool NEXT>
+  // goes to buffer 1 - SB (masked first when its keys end inside it:
+  // mask_next) and, with TRACK, its row max to mt. The DMA job is issued in
+  // its slots.
+  template <int SB, bool NEXT, bool TRACK>
   __device__ __forceinline__ void tile(uint32_t dstage, bool mask_next, int kb_next, int klen,
                                        const KVDma& dma) {
     constexpr int NB = 1 - SB;
@@ -430,7 +434,7 @@ struct FwdWave {
         if constexpr (exp_slot(u) + 2 == g) this->template p_pack<u>(fe);
       });
       // Row max of tile t+1.
-      if constexpr (NEXT && g >= kMaxSlot0) {
+      if constexpr (NEXT && TRACK && g >= kMaxSlot0) {
         this->template max_step<NB, g - kMaxSlot0>(mx);
         asm volatile("" : "+v"(mx[0]), "+v"(mx[1]));
       }
@@ -453,7 +457,7 @@ struct FwdWave {
     keep_alive(vq[15 % kVQ]);
     keep_alive(pb[3][1]);
     advance_v(dstage);
-    if constexpr (NEXT) {
+    if constexpr (NEXT && TRACK) {
       mt[0] = pair_max(mx[0]);
       mt[1] = pair_max(mx[1]);
     }
@@ -500,6 +504,22 @@ struct FwdWave {
     }
   }
 
+  // After a pass that kept every row's first-tile max as m (no per-tile max,
+  // no rescale): whether every row sum is at most 2^64 (so every p was
+  // finite and 1/l is a normal number) and every O^T accumulator finite.
+  // Then the result is the one a running max gives, up to fp32 rounding: m
+  // only sets the exponent range. Reads O, so after fence_o().
+  __device__ __forceinline__ bool sums_in_range() const {
+    float mo = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+        for (int r = 0; r < 16; r += 2) mo = max3abs(mo, o[dt][qb][r], o[dt][qb][r + 1]);
+    return lsum[0][0] <= 0x1p64f && lsum[1][0] <= 0x1p64f && mo <= 0x1.fffffep127f;
+  }
+
   // O (or the range's partial O) of query block qb: O / l, optional padding
   // correction, bf16, out through the 8 KB staging area `stage` (tile_io.h
   // row staging, 4 whole 256-byte rows per store); LSE in fp32.
@@ -518,14 +538,48 @@ struct FwdWave {
   }
 };
 
-// One workgroup per work item (256 queries of one (batch, head)), or per key
-// range of one of the last work items when they are split.
-__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(1, 1)))
-void attn_fwd_kernel(FwdParams p) {
-  __shared__ __attribute__((aligned(1024))) bf16 kv_lds[kStages * 2 * kTileElems];
+// Exponent range. attn_fwd_kernel keeps every row's max at its first key
+// tile's for the whole range (no per-tile max and no rescale: ~34 VALU
+// instructions fewer per tile and wave), so p = exp2((s - m) c) only stays
+// finite while no later score exceeds that max by ~64 in log2 units. m only
+// sets the exponent range: the result is the one a running max gives, up to
+// fp32 rounding, as long as every p, every row sum and O stay finite, which
+// FwdWave::sums_in_range() checks after the pass. A workgroup with a row that
+// failed it writes kRerunMark in place of its output, and
+// attn_fwd_fixup_kernel, launched right after on the same stream, reads every
+// block's mark place and runs the marked ones again with the running max and
+// the lazy rescale (fwd_block<true>, the form every tile had before).
+//
+// The mark: a NaN that no arithmetic here produces (a bf16 conversion of a
+// NaN gives 0x7fc0), in the first element of the block's output, the O row
+// of its first query or its key range's partial O record. The first launch
+// writes every block's output or its mark, so the mark place never holds a
+// stale value; an output that holds the mark's bits anyway only costs an
+// exact second run of its block.
+constexpr uint16_t kRerunMark = 0x7fc1;
 
+__device__ __forceinline__ int64_t part_record(const FwdParams& p, int item_idx, int split) {
+  return (int64_t)(item_idx - p.full_blocks) * p.nsplit + split;
+}
+
+__device__ __forceinline__ uint16_t* mark_ptr(const FwdParams& p, int item_idx, int split) {
+  const int qblk = item_idx % p.nqblk, bh = item_idx / p.nqblk;
+  const int b = bh / p.H, h = bh - b * p.H;
+  return reinterpret_cast<uint16_t*>(
+      split < 0 ? p.o + b * p.os0 + (int64_t)qblk * kQPerWg * p.os1 + h * p.os2
+                : p.part_o + part_record(p, item_idx, split) * kQPerWg * kD);
+}
+
+// One workgroup's work: block blk's work item (256 queries of one (batch,
+// head)), or one key range of one of the last work items when they are split.
+// TRACK: the running max with the lazy rescale, else the first tile's max
+// (and the mark when a row leaves the range).
+template <bool TRACK>
+__device__ __forceinline__ void fwd_block(const FwdParams& p, int blk, bf16* kv_lds) {
   int item_idx, split;
-  block_item(p, item_idx, split);
+  block_item(p, blk, item_idx, split);
+  const int64_t part_row = part_record(p, item_idx, split);
+  uint16_t* mark = mark_ptr(p, item_idx, split);
   const Item it = decode_item(p, item_idx);
   // Key tiles [t0, t0 + ntiles) of the item.
   int t0 = 0, ntiles = it.ntiles;
@@ -602,8 +656,9 @@ void attn_fwd_kernel(FwdParams p) {
       constexpr bool NEXT = decltype(next)::value;
       top(t);
       const int kbn = (t0 + t + 1) * kBN;
-      w.tile<SB, NEXT>(stage_addr(t + 1) - stage_addr(t), kbn + kBN > it.klen, kbn, it.klen, dma);
-      if constexpr (NEXT) w.update_max();
+      w.tile<SB, NEXT, TRACK>(stage_addr(t + 1) - stage_addr(t), kbn + kBN > it.klen, kbn, it.klen,
+                              dma);
+      if constexpr (NEXT && TRACK) w.update_max();
     };
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
@@ -621,8 +676,23 @@ void attn_fwd_kernel(FwdParams p) {
   wait_dma();
   __syncthreads();  // every wave is done with the ring; no DMA in flight
 
-  // Output through the ring: 16 KB per wave.
   w.fence_o();
+  if constexpr (!TRACK) {
+    if (ntiles > 0) {
+      // Every wave's verdict through LDS (ring stage 3; the output staging
+      // uses stages 0-1).
+      int* flags = reinterpret_cast<int*>(kv_lds + 3 * 2 * kTileElems);
+      const bool out_of_range = !w.sums_in_range();
+      if (lane == 0) flags[wave] = __builtin_amdgcn_ballot_w64(out_of_range) != 0;
+      __syncthreads();
+      if (__builtin_amdgcn_readfirstlane(flags[0] | flags[1] | flags[2] | flags[3])) {
+        if (tid == 0) *mark = kRerunMark;
+        return;
+      }
+    }
+  }
+
+  // Output through the ring: 16 KB per wave.
   bf16* stage = kv_lds + wave * 8192;
   if (split < 0) {
     const bool pad = p.ln_pad != nullptr;
@@ -636,7 +706,7 @@ void attn_fwd_kernel(FwdParams p) {
       if (qrow0 + 32 + w.li < p.Sq) lp[qrow0 + 32 + w.li] = lse1;
     }
   } else {
-    const int64_t row = (int64_t)(item_idx - p.full_blocks) * p.nsplit + split;
+    const int64_t row = part_row;
     bf16* obase = p.part_o + row * kQPerWg * kD;
     const int q0 = wave * kQPerWave;
     const float lse0 = w.finish<0>(0.f, false, obase, kD, q0, kQPerWg, lane, stage);
@@ -644,6 +714,49 @@ void attn_fwd_kernel(FwdParams p) {
     if (w.hh == 0) {
       p.part_lse[row * kQPerWg + q0 + w.li] = lse0;
       p.part_lse[row * kQPerWg + q0 + 32 + w.li] = lse1;
+    }
+  }
+}
+
+// One block per workgroup: TRACK false is the first-tile-max form, which
+// attn_fwd_fixup_kernel must follow; TRACK true the running max (one launch).
+template <bool TRACK>
+__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void attn_fwd_kernel(FwdParams p) {
+  __shared__ __attribute__((aligned(1024))) bf16 kv_lds[kStages * 2 * kTileElems];
+  fwd_block<TRACK>(p, blockIdx.x, kv_lds);
+}
+
+// The fix-up launch: at most one workgroup per CU (one round), workgroup g
+// taking blocks g, g + G, g + 2 G, ... (G = gridDim.x), 64 at a time: wave 0
+// loads their mark places (one lane each) and the workgroup runs the marked
+// blocks one after another. Without marks every workgroup exits after one
+// load per lane; with every block marked the work is one more pass over the
+// grid.
+__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void attn_fwd_fixup_kernel(FwdParams p, int nblocks) {
+  __shared__ __attribute__((aligned(1024))) bf16 kv_lds[kStages * 2 * kTileElems];
+  __shared__ uint64_t marked;
+  for (int base = blockIdx.x; base < nblocks; base += 64 * gridDim.x) {
+    if (threadIdx.x < 64) {
+      const int blk = base + (int)threadIdx.x * (int)gridDim.x;
+      bool m = false;
+      if (blk < nblocks) {
+        int item_idx, split;
+        block_item(p, blk, item_idx, split);
+        m = *mark_ptr(p, item_idx, split) == kRerunMark;
+      }
+      const uint64_t bal = __builtin_amdgcn_ballot_w64(m);
+      if (threadIdx.x == 0) marked = bal;
+    }
+    __syncthreads();
+    uint64_t todo = marked;
+    __syncthreads();  // every wave has read `marked` before the next chunk
+    while (todo) {
+      const int i = __builtin_ctzll(todo);
+      todo &= todo - 1;
+      fwd_block<true>(p, base + i * (int)gridDim.x, kv_lds);
+      __syncthreads();  // the ring is free for the next block
     }
   }
 }
@@ -867,6 +980,22 @@ static int fwd_kernel_choice(int64_t Sk) {
   return Sk <= kPingPongMaxSk ? 0 : 1;
 }
 
+// Which form of the one-wave kernel runs: the first-tile max (true) saves
+// ~3% of the tile loop but needs the fix-up launch after it, which costs
+// ~4.7 us even when it finds nothing to do (MI355X, kernel trace), so it pays
+// from about one round of 64-tile work items on: more rounds of blocks than
+// CUs, or longer key ranges. Measured (median, one process): B=1 4096 tokens
+// (one round of 64 tiles) at par; B=2 233.8 -> 229.0 us, B=16 1883 -> 1826
+// us, 9216 tokens 617 -> 580 us. AA_FWD_FIRST_TILE_MAX=0|1 forces one.
+static bool fwd_first_tile_max(const FwdParams& p, int blocks) {
+  const char* e = std::getenv("AA_FWD_FIRST_TILE_MAX");
+  if (e && *e) return e[0] != '0';
+  const int ncu = std::max(device_cu_count(), 1);
+  const int64_t rounds = (blocks + ncu - 1) / ncu;
+  const int64_t tiles = ((int64_t)p.Sk + kBN - 1) / kBN;
+  return rounds * tiles > 64;
+}
+
 extern "C" int aa_attn_fwd(const aa_attn_fwd_args* a, void* stream);
 
 extern "C" int aa_attn_fwd_noalloc(const aa_attn_fwd_args* a, void* stream) {
@@ -903,7 +1032,15 @@ extern "C" int aa_attn_fwd(const aa_attn_fwd_args* a, void* stream) {
   const int which = fwd_kernel_choice(p.Sk);
   if (which < 0) return fail(AA_EINVAL, "AA_FWD_KERNEL must be pp or 1w");
   if (which == 0) launch_attn_fwd_pp(p, (unsigned)blocks, st);
-  else attn_fwd_kernel<<<dim3((unsigned)blocks), kWaves * 64, 0, st>>>(p);
+  else if (fwd_first_tile_max(p, blocks)) {
+    attn_fwd_kernel<false><<<dim3((unsigned)blocks), kWaves * 64, 0, st>>>(p);
+    if (int rc = check_launch("attn_fwd")) return rc;
+    // Re-runs the blocks whose rows left the first tile's exponent range.
+    const int fix_groups = std::min(blocks, std::max(device_cu_count(), 1));
+    attn_fwd_fixup_kernel<<<dim3((unsigned)fix_groups), kWaves * 64, 0, st>>>(p, blocks);
+  } else {
+    attn_fwd_kernel<true><<<dim3((unsigned)blocks), kWaves * 64, 0, st>>>(p);
+  }
   if (int rc = check_launch("attn_fwd")) return rc;
   if (p.split_items > 0) {
     const int groups = (p.split_items * kQPerWg + kCombineQ - 1) / kCombineQ;

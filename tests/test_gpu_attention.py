@@ -7,7 +7,9 @@ values.
 
 from __future__ import annotations
 
+import ctypes
 import math
+import sys
 
 import pytest
 import torch
@@ -23,6 +25,10 @@ BF = torch.bfloat16
 # that weight V (so the output is exactly normalised); it differs from the
 # fp32 logsumexp by ~2^-9 / sqrt(#keys) relative in the sum, i.e. < 1e-3 in lse.
 LSE_TOL = dict(max_abs=2e-3, rel_l2=2e-4)
+# A row whose softmax sits on one key carries that key's bf16-rounded p into the
+# sum undiluted: up to 2^-8 relative (half an ulp just above a power of two),
+# ln(1 + 2^-8) = 3.9e-3 in lse, unless m equals that key's score exactly.
+LSE_TOL_PEAKED = dict(max_abs=4e-3, rel_l2=2e-4)
 
 
 def _qkv(B, Sq, Sk, H, seed, hd=128):
@@ -100,6 +106,104 @@ def test_attention_large_logits(pkg):
     out = pkg.attention(*_gpu(q, k, v))
     torch.cuda.synchronize()
     parity(out, ref.attention_sdpa(q, k, v).reshape(B, S, H * 128), name="large logits")
+
+
+def _spiked(B, Sq, Sk, H, delta, hot, seed):
+    """N(0,1) q, k, v plus a shared unit direction u: every q row gets delta * u and
+    the keys at positions `hot` become 20 u. A hot key's score then exceeds the
+    other keys' (delta * N(0,1) along u) by ~17.6 delta, i.e. ~2.24 delta in log2
+    units at scale 1/sqrt(128): past 64 from delta ~29, past 128 (p = inf with
+    the first tile's max) from delta ~57."""
+    q, k, v = _qkv(B, Sq, Sk, H, seed)
+    g = torch.Generator().manual_seed(seed + 1)
+    u = torch.randn(128, generator=g)
+    u = u / u.norm()
+    q = (q + delta * u).to(BF).float()
+    k = k.clone()
+    k[:, hot] = (20.0 * u).to(BF).float()
+    return q, k, v
+
+
+# Forward kernel forms: (AA_FWD_KERNEL, AA_FWD_FIRST_TILE_MAX); "1w" picks its
+# form by the amount of work, "1w-ftm" forces the first-tile max with the fix-up
+# launch, "1w-run" the running max.
+FWD_FORMS = {"pp": ("pp", None), "1w": ("1w", None), "1w-ftm": ("1w", "1"), "1w-run": ("1w", "0")}
+
+
+def _set_form(monkeypatch, form):
+    kernel, ftm = FWD_FORMS[form]
+    monkeypatch.setenv("AA_FWD_KERNEL", kernel)
+    if ftm is None:
+        monkeypatch.delenv("AA_FWD_FIRST_TILE_MAX", raising=False)
+    else:
+        monkeypatch.setenv("AA_FWD_FIRST_TILE_MAX", ftm)
+
+
+def _clear_form(monkeypatch):
+    monkeypatch.delenv("AA_FWD_KERNEL", raising=False)
+    monkeypatch.delenv("AA_FWD_FIRST_TILE_MAX", raising=False)
+
+
+@pytest.mark.parametrize("form", ["pp", "1w-ftm", "1w-run"])
+@pytest.mark.parametrize("delta", [12.0, 33.0, 60.0])
+@pytest.mark.parametrize(
+    "B,Sq,Sk,H,lens,hot",
+    [
+        # 4 work items: split into 8 key ranges of 8 tiles; hot keys inside the
+        # ranges of keys 2048-2559 and 3584-4095, past their first tiles.
+        (1, 300, 4096, 2, None, [2118, 4091]),
+        # 200 work items, no split (checked on sampled rows).
+        (1, 2048, 2500, 25, None, [1000]),
+        # key lengths: batch 1's key 2200 lies past its length (masked).
+        (2, 300, 3000, 2, [3000, 1500], [900, 2200]),
+    ],
+)
+def test_scores_far_above_the_first_tile(pkg, monkeypatch, form, delta, B, Sq, Sk, H, lens, hot):
+    """Rows whose later scores exceed their first key tile's max by ~27, ~74 and
+    ~134 in log2 units. The one-wave kernel's first-tile-max form keeps the first
+    tile's max for the whole range: at ~27 its sums stay in range, at ~74 the row
+    sums pass 2^64, at ~134 p overflows; the latter two write the rerun mark and
+    the fix-up launch runs the item again with the running max. Every form is
+    held to the oracle like any input; the LSE of these one-key rows to the bf16
+    bound of LSE_TOL_PEAKED."""
+    q, k, v = _spiked(B, Sq, Sk, H, delta, hot, seed=4400 + Sq + H)
+    seq = torch.tensor(lens, dtype=torch.int32) if lens is not None else None
+    _set_form(monkeypatch, form)
+    qd, kd, vd = _gpu(q, k, v)
+    if seq is None:
+        out, lse = torch.ops.anima_flat.fa_fwd(qd, kd, vd)
+    else:
+        out, lse = torch.ops.anima_flat.fa_fwd_k(qd, kd, vd, seq.to("cuda"))
+    torch.cuda.synchronize()
+    _clear_form(monkeypatch)
+    rows = torch.arange(Sq) if Sq <= 512 else torch.randperm(Sq, generator=torch.Generator().manual_seed(7))[:96]
+    eo, el = ref.attention_lse(q[:, rows], k, v, seq)
+    tag = f"{form} delta={delta} B{B} Sq{Sq} Sk{Sk} H{H} lens={lens}"
+    parity(out[:, rows], eo, name=tag)
+    parity(lse[:, :, rows], el, **LSE_TOL_PEAKED, name=f"lse {tag}")
+
+
+def test_stale_rerun_mark_in_output(pkg, dev, monkeypatch):
+    """An output buffer that already holds the rerun mark everywhere (as a reused
+    allocation might) is overwritten: the first-tile-max launch writes every element
+    of a work item whose sums stayed in range, so the fix-up launch finds no mark."""
+    _set_form(monkeypatch, "1w-ftm")
+    A = sys.modules[pkg.__name__ + ".attention"]
+    L = pkg._lib
+    B, S, H = 1, 512, 2
+    q, k, v = _qkv(B, S, 4096, H, seed=77)
+    qd, kd, vd = _gpu(q, k, v)
+    out = torch.full((B, S, H, 128), 0x7FC1, dtype=torch.int16, device=dev).view(BF)
+    args = A._fwd_args(qd, kd, vd, out, None, None, None)
+    ws = None
+    need = L.lib().aa_attn_fwd_workspace(B, S, 4096, H, 128)
+    if need:
+        ws = torch.empty(need, dtype=torch.uint8, device=dev)
+        args.workspace, args.workspace_bytes = ws.data_ptr(), need
+    L.check(L.lib().aa_attn_fwd(ctypes.byref(args), L.stream(qd)), "attn_fwd")
+    torch.cuda.synchronize()
+    _clear_form(monkeypatch)
+    parity(out, ref.attention_sdpa(q, k, v).reshape(B, S, H, 128), name="stale mark")
 
 
 @pytest.mark.parametrize(
@@ -366,7 +470,7 @@ def test_cross_attention_backward_training_shape(pkg):
     parity(out.reshape(B, Sq, H, 128)[:, qrows], eo, name="cross fwd (sampled rows)")
 
 
-@pytest.mark.parametrize("kernel", ["pp", "1w"])
+@pytest.mark.parametrize("kernel", ["pp", "1w", "1w-ftm", "1w-run"])
 @pytest.mark.parametrize(
     "B,Sq,Sk,H,lens",
     [
@@ -379,18 +483,20 @@ def test_cross_attention_backward_training_shape(pkg):
 )
 def test_both_forward_kernels(pkg, monkeypatch, kernel, B, Sq, Sk, H, lens):
     """aa_attn_fwd runs the two-group kernel up to 2048 keys and the one-wave-per-SIMD
-    kernel beyond (AA_FWD_KERNEL forces one); each is held to the oracle on every
-    shape, with and without key lengths, and its LSE."""
+    kernel beyond (AA_FWD_KERNEL forces one), the latter in its first-tile-max form
+    (with the fix-up launch) from about a round of 64-tile work items on and with the
+    running max below (AA_FWD_FIRST_TILE_MAX forces one); each is held to the oracle
+    on every shape, with and without key lengths, and its LSE."""
     q, k, v = _qkv(B, Sq, Sk, H, seed=9000 + Sq + Sk + H)
     seq = torch.tensor(lens, dtype=torch.int32) if lens is not None else None
-    monkeypatch.setenv("AA_FWD_KERNEL", kernel)
+    _set_form(monkeypatch, kernel)
     qd, kd, vd = _gpu(q, k, v)
     if seq is None:
         out, lse = torch.ops.anima_flat.fa_fwd(qd, kd, vd)
     else:
         out, lse = torch.ops.anima_flat.fa_fwd_k(qd, kd, vd, seq.to("cuda"))
     torch.cuda.synchronize()
-    monkeypatch.delenv("AA_FWD_KERNEL")
+    _clear_form(monkeypatch)
     eo, el = ref.attention_lse(q, k, v, seq)
     tag = f"{kernel} B{B} Sq{Sq} Sk{Sk} H{H} lens={lens}"
     parity(out, eo, name=tag)
