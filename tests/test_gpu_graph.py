@@ -11,6 +11,7 @@ from __future__ import annotations
 import pytest
 import torch
 
+from conftest import parity
 from oracle import attn_oracle as ref
 
 pytestmark = pytest.mark.gpu
@@ -112,3 +113,56 @@ def test_graph_replays_split_backward_and_projections(pkg, proj):
             torch.cuda.synchronize()
             for j, (a, e) in enumerate(zip(outs, eager)):
                 assert torch.equal(a, e), f"replay {i}: output {j} {a.dtype} {tuple(a.shape)} differs"
+
+
+def test_graph_replays_first_tile_max_with_fixup(pkg, monkeypatch):
+    """The one-wave forward's first-tile-max form (forced) under capture: its two
+    launches, on ordinary inputs and on inputs whose later scores overflow the first
+    tile's exponent range, so that the captured fix-up launch re-runs marked blocks
+    on every replay. Replays equal the eager outputs bit for bit and the oracle."""
+    dev = torch.device("cuda:0")
+    d = 128
+    g = torch.Generator().manual_seed(93)
+    q0, k0, v0 = (ref.bf16_normal((1, 512, 2, d), g) for _ in range(3))
+    # Spiked: every query gets 60 u, keys 1500 and 3000 become 20 u (u a unit
+    # vector): their scores exceed the first tile's max by ~134 in log2 units.
+    qs = ref.bf16_normal((1, 300, 2, d), g)
+    ks = ref.bf16_normal((1, 3100, 2, d), g)
+    vs = ref.bf16_normal((1, 3100, 2, d), g)
+    u = torch.randn(d, generator=g)
+    u = u / u.norm()
+    qs = (qs + 60.0 * u).to(BF).float()
+    ks[:, [1500, 3000]] = (20.0 * u).to(BF).float()
+    k0 = torch.cat([k0, ref.bf16_normal((1, 4096 - 512, 2, d), g)], dim=1)
+    v0 = torch.cat([v0, ref.bf16_normal((1, 4096 - 512, 2, d), g)], dim=1)
+    args0 = [t.to(dev, BF) for t in (q0, k0, v0)]
+    args1 = [t.to(dev, BF) for t in (qs, ks, vs)]
+    monkeypatch.setenv("AA_FWD_KERNEL", "1w")
+    monkeypatch.setenv("AA_FWD_FIRST_TILE_MAX", "1")
+
+    def step():
+        o0, l0 = torch.ops.anima_flat.fa_fwd(*args0)
+        o1, l1 = torch.ops.anima_flat.fa_fwd(*args1)
+        return [o0, l0, o1, l1]
+
+    with torch.no_grad():
+        eager = [t.clone() for t in step()]
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            step()
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            outs = step()
+        for i in range(3):
+            torch.ops.anima_flat.fa_fwd_nolse(*(ref.bf16_normal((1, 700, 3, d), g).to(dev, BF) for _ in range(3)))
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            for j, (a, e) in enumerate(zip(outs, eager)):
+                assert torch.equal(a, e), f"replay {i}: output {j} {a.dtype} {tuple(a.shape)} differs"
+    monkeypatch.delenv("AA_FWD_KERNEL")
+    monkeypatch.delenv("AA_FWD_FIRST_TILE_MAX")
+    parity(eager[0], ref.attention_lse(q0, k0, v0)[0], name="first-tile max, ordinary rows")
+    parity(eager[2], ref.attention_lse(qs, ks, vs)[0], name="first-tile max, fixed-up rows")
