@@ -74,6 +74,8 @@ def _both(pkg, B, Sq, Sk, H, seed, lens=None, hd=128):
         (1, 1024, 1024, 16, None, True, 128),  # config 1: 64 work items, split 4 ways
         (1, 300, 200, 3, [150], True, 128),  # smaller, masked with the padding correction
         (1, 4096, 4096, 16, None, False, 128),  # config 2: one full round, no partials
+        # 9216 keys: the first-tile-max form with its fix-up launch, 72 items x 3 key ranges
+        (1, 9216, 9216, 2, None, True, 128),
         (1, 16384, 16384, 1, None, True, 384),  # the VAE attention: 128 items x 2 key ranges
         (1, 4096, 4096, 1, None, True, 384),  # smaller again: 32 items x 8 key ranges
     ],
