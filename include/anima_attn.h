@@ -208,6 +208,11 @@ size_t aa_attn_fwd_workspace(int64_t B, int64_t Sq, int64_t Sk, int64_t H, int64
  * keys j >= seqused_k[b] are excluded when seqused_k != NULL; lse is the
  * natural-log row log-sum-exp of the scaled scores over the attended keys.
  * One kernel launch, plus a combine pass when aa_attn_fwd_workspace() > 0.
+ * From about two rounds of 64-tile work items on (e.g. B=2 at 4096 keys),
+ * the hd-128 forward keeps each row's first key tile max and follows its
+ * launch with a fix-up launch that re-runs, with a running max, the work
+ * items whose scores left that exponent range (AA_FWD_FIRST_TILE_MAX=0|1
+ * forces the form). Every launch goes to `stream`; none allocates.
  * Replaces: src/attention.py:43-53 (anima_flat::fa_fwd),
  *           src/attention.py:63-66 (anima_flat::fa_fwd_nolse),
  *           src/attention.py:74-81 (anima_flat::fa_fwd_k), and with
