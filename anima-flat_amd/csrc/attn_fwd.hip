@@ -548,14 +548,15 @@ struct FwdWave {
 // failed it writes kRerunMark in place of its output, and
 // attn_fwd_fixup_kernel, launched right after on the same stream, reads every
 // block's mark place and runs the marked ones again with the running max and
-// the lazy rescale (fwd_block<true>, the form every tile had before).
+// the lazy rescale (fwd_block<true>, the form attn_fwd_kernel<true> runs alone
+// where one launch is cheaper).
 //
-// The mark: a NaN that no arithmetic here produces (a bf16 conversion of a
-// NaN gives 0x7fc0), in the first element of the block's output, the O row
-// of its first query or its key range's partial O record. The first launch
-// writes every block's output or its mark, so the mark place never holds a
-// stale value; an output that holds the mark's bits anyway only costs an
-// exact second run of its block.
+// The mark: a NaN with a payload (the default quiet NaN converts to bf16
+// 0x7fc0), in the first element of the block's output, the O row of its
+// first query or its key range's partial O record. The first launch writes
+// every block's output or its mark, so the mark place never holds a stale
+// value; an output that holds the mark's bits anyway (a NaN input can carry
+// that payload through) only costs an exact second run of its block.
 constexpr uint16_t kRerunMark = 0x7fc1;
 
 __device__ __forceinline__ int64_t part_record(const FwdParams& p, int item_idx, int split) {
