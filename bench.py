@@ -6,15 +6,16 @@ B=1 self-attention, non-causal, q/k/v from the QK-RMSNorm + 3D-RoPE
 prologue on N(0,1) QKV), plus the per-denoiser-step attention time.
 
 A "step" is one call of the attention forward op (anima_flat::fa_fwd_nolse)
-over the config-2 batch, inputs resident in HBM; it launches two kernels,
-attn_fwd_kernel and attn_fwd_fixup_kernel (which re-runs the work items whose
-rows left the first key tile's exponent range: none on this data; it reads
-one value per item and exits). Timing: W untimed steps, then K steps bracketed
-by torch.cuda.synchronize(); `value` = algorithmic FLOPs (4*B*H*Sq*Sk*d) per
-step / mean wall-clock step time. `roofline.achieved` is the same FLOPs over
-the mean duration of one aa_attn_fwd call (both launches), from HIP events on
-the launch stream around K calls made straight through the C ABI (no torch
-allocation in between). `roofline.traffic` is read from the committed rocprofv3 PMC summary
+over the config-2 batch, inputs resident in HBM; it launches one kernel,
+attn_fwd_kernel in its running-max form (one round of 64-tile work items: the
+first-tile-max form, with its fix-up launch attn_fwd_fixup_kernel, only pays
+from about two rounds on, as in the B=16 and 9216-token extras). Timing: W
+untimed steps, then K steps bracketed by torch.cuda.synchronize(); `value` =
+algorithmic FLOPs (4*B*H*Sq*Sk*d) per step / mean wall-clock step time.
+`roofline.achieved` is the same FLOPs over the mean duration of one
+aa_attn_fwd call (all its launches), from HIP events on the launch stream
+around K calls made straight through the C ABI (no torch allocation in
+between). `roofline.traffic` is read from the committed rocprofv3 PMC summary
 profiles/attn_fwd_cfg2_pmc.txt.
 
 Extra fields report the other kernels of the path: prologue and head_norm
@@ -410,7 +411,7 @@ def main() -> int:
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
             "traffic": pmc_traffic("attn_fwd_cfg2_pmc.txt"),
-            "kernel": "attn_fwd_kernel + attn_fwd_fixup_kernel",
+            "kernel": "attn_fwd_kernel",
             "kernel_us": round(attn_ms * 1e3, 2),
         },
     }
