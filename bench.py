@@ -467,7 +467,7 @@ def main() -> int:
                 "GB/s": round(2 * 2 * S * H * d * 2 / (us_hn * 1e-3) / 1e9, 1),
             }
 
-            # Configs 1 and 4 (§8(d) table): self-attention forward % of peak and the
+            # Configs 1 and 4: self-attention forward % of peak and the
             # prologue's GB/s at B=1 S=1024 (launch-latency regime), B=16 S=4096 and
             # B=1 S=9216 (96x96 latent).
             fwd_nolse = torch.ops.anima_flat.fa_fwd_nolse
