@@ -183,6 +183,48 @@ def test_scores_far_above_the_first_tile(pkg, monkeypatch, form, delta, B, Sq, S
     parity(lse[:, :, rows], el, **LSE_TOL_PEAKED, name=f"lse {tag}")
 
 
+def _random_long_cases(n, seed):
+    """Seeded (B, Sq, Sk, H, lens, hot, delta): key ranges past 2048 (the one-wave
+    kernel), ragged query and key counts, optional per-batch key lengths, and hot
+    keys (scores ~2.24 delta log2 units above the rest) at random positions."""
+    g = torch.Generator().manual_seed(seed)
+    out = []
+    for _ in range(n):
+        B = int(torch.randint(1, 4, (1,), generator=g))
+        H = int(torch.randint(1, 4, (1,), generator=g))
+        Sq = int(torch.randint(1, 600, (1,), generator=g))
+        Sk = int(torch.randint(2049, 4200, (1,), generator=g))
+        lens = None
+        if int(torch.randint(0, 2, (1,), generator=g)):
+            lens = [int(torch.randint(1, Sk + 1, (1,), generator=g)) for _ in range(B)]
+        hot = sorted({int(torch.randint(0, Sk, (1,), generator=g)) for _ in range(3)})
+        delta = [0.0, 20.0, 40.0, 70.0][int(torch.randint(0, 4, (1,), generator=g))]
+        out.append((B, Sq, Sk, H, lens, hot, delta))
+    return out
+
+
+@pytest.mark.parametrize("B,Sq,Sk,H,lens,hot,delta", _random_long_cases(10, seed=3003))
+def test_random_first_tile_max_cases(pkg, monkeypatch, B, Sq, Sk, H, lens, hot, delta):
+    """The first-tile-max form (forced) with its fix-up launch on seeded random shapes:
+    key splits over partial last rounds, ragged tiles, key lengths that cut or skip the
+    hot keys, and rows whose scores stay in range (delta 0, 20), pass 2^64 (40) or
+    overflow (70). Out and LSE against the oracle."""
+    q, k, v = _spiked(B, Sq, Sk, H, delta, hot, seed=5000 + Sq + Sk)
+    seq = torch.tensor(lens, dtype=torch.int32) if lens is not None else None
+    _set_form(monkeypatch, "1w-ftm")
+    qd, kd, vd = _gpu(q, k, v)
+    if seq is None:
+        out, lse = torch.ops.anima_flat.fa_fwd(qd, kd, vd)
+    else:
+        out, lse = torch.ops.anima_flat.fa_fwd_k(qd, kd, vd, seq.to("cuda"))
+    torch.cuda.synchronize()
+    _clear_form(monkeypatch)
+    eo, el = ref.attention_lse(q, k, v, seq)
+    tag = f"B{B} Sq{Sq} Sk{Sk} H{H} lens={lens} hot={hot} delta={delta}"
+    parity(out, eo, name=tag)
+    parity(lse, el, **LSE_TOL_PEAKED, name=f"lse {tag}")
+
+
 def test_stale_rerun_mark_in_output(pkg, dev, monkeypatch):
     """An output buffer that already holds the rerun mark everywhere (as a reused
     allocation might) is overwritten: the first-tile-max launch writes every element
