@@ -618,9 +618,13 @@ __device__ __forceinline__ void fwd_block(const FwdParams& p, int blk, bf16* kv_
   if (ntiles > 0) {
     issue_job(0);
     issue_job(1);
+    // The Q rows and tile 0 (tile 1's 8 instructions may still be in
+    // flight: the first tile's top waits for them).
+    asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+  } else {
+    wait_dma();
   }
-  wait_dma();
-  __syncthreads();  // tiles 0 and 1 from every wave
+  __syncthreads();  // Q rows and tile 0 from every wave
   w.read_q(qstage, lane);
   __syncthreads();  // every wave has read its Q rows
   if (ntiles > 0) {
