@@ -442,9 +442,14 @@ void dkdv1w_kernel(Params p, int nkblk, int total_blocks) {
   if (ntiles > 0) {
     issue_job(0);
     issue_job(1);
+    // The K / V rows and tile 0 (tile 1's job, issued last, may still be in
+    // flight: the first tile's top waits for it).
+    if (stats_dma) asm volatile("s_waitcnt vmcnt(9)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+  } else {
+    wait_dma();
   }
-  wait_dma();
-  __syncthreads();  // tiles 0 and 1 and every wave's K / V rows
+  __syncthreads();  // tile 0 and every wave's K / V rows
   w.read_kv(kst, kst + 4096, lane);
   __syncthreads();  // every wave has read its K / V rows
   if (ntiles > 0) {
